@@ -1,0 +1,283 @@
+"""Benchmark: one fast-matmul Linear per step on one MI355X, vs native BF16.
+
+Default workload: rank-7 dynamic plan, MLP-up
+linear M x K x N = 4096 x 4096 x 12288, x ~ N(0,1) BF16, weight[N, K] ~
+N(0, 1/K) BF16, no bias, FP16 leaves, output allocated per call, workspace
+reused. Inputs are generated on the CPU with a seeded torch.Generator and
+copied to HBM before timing. Other configurations: --config c3|c4|c5|c5-rank7|
+c5-rank49|c3-rank48.
+
+Prints ONE JSON line (the driver's contract). ``value`` is effective TFLOP/s
+= 2*M*N*K / t over the K timed steps; ``roofline`` is measured for the leaf
+product kernel (the dominant one) with HIP events on the stream it runs on;
+``cpu_baseline`` times the CPU oracle (the reference's scheme evaluation
+restated in numpy) on a bounded row sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+from pathlib import Path
+import sys
+import time
+
+REPO_ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO_ROOT / "rdna3-fastmm_amd"))
+
+import torch  # noqa: E402
+
+METRIC = "ms and effective TFLOP/s per linear vs native BF16 GEMM (speedup), 1 MI355X"
+MFMA_FP16_PEAK_TFLOPS = 2500.0
+HBM_PEAK_GBPS = 8000.0
+
+CONFIGS = {
+    "c2": dict(scheme="rank7", rows=4096, inner=4096, columns=12288, bias=False, prepacked=False,
+               name="rank7-dynamic-mlp-up-4096x4096x12288"),
+    "c3": dict(scheme="rank7", rows=8214, inner=12288, columns=4608, bias=True, prepacked=True,
+               name="rank7-prepacked-mlp-down-8214x12288x4608-bias"),
+    "c3-rank48": dict(scheme="rank48", rows=8214, inner=12288, columns=4608, bias=False, prepacked=True,
+                      name="rank48-prepacked-8214x12288x4608"),
+    "c4": dict(scheme="rank49", rows=19968, inner=4096, columns=16384, bias=True, prepacked=True,
+               name="rank49-prepacked-mlp-up-19968x4096x16384-bias"),
+    "c5": dict(scheme="rank48", rows=8192, inner=8192, columns=8192, bias=False, prepacked=True,
+               name="rank48-prepacked-square-8192"),
+    "c5-rank7": dict(scheme="rank7", rows=8192, inner=8192, columns=8192, bias=False, prepacked=True,
+                     name="rank7-prepacked-square-8192"),
+    "c5-rank49": dict(scheme="rank49", rows=8192, inner=8192, columns=8192, bias=False, prepacked=True,
+                      name="rank49-prepacked-square-8192"),
+}
+
+
+def _inputs(cfg: dict, seed: int = 0):
+    g = torch.Generator().manual_seed(seed)
+    m, k, n = cfg["rows"], cfg["inner"], cfg["columns"]
+    x = torch.randn((m, k), generator=g).to(torch.bfloat16)
+    w = (torch.randn((n, k), generator=g) / k**0.5).to(torch.bfloat16)
+    b = (torch.randn((n,), generator=g) * 0.02).to(torch.bfloat16) if cfg["bias"] else None
+    return x, w, b
+
+
+def _time_region(fn, steps: int) -> float:
+    """ms per call over `steps` calls, synchronized on both sides."""
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - start) * 1e3 / steps
+
+
+def _event_ms(fn, repeats: int) -> list[float]:
+    """Per-call HIP-event durations on the current stream (where our kernels run)."""
+    out = []
+    for _ in range(repeats):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        fn()
+        end.record()
+        end.synchronize()
+        out.append(start.elapsed_time(end))
+    return out
+
+
+def _median(values: list[float]) -> float:
+    ordered = sorted(values)
+    return ordered[len(ordered) // 2]
+
+
+def cpu_baseline(cfg: dict, x, w, b, budget_s: float) -> dict:
+    """Time the CPU oracle on a row sample of the workload; TFLOP/s of that sample."""
+    import numpy as np
+    from threadpoolctl import threadpool_info, threadpool_limits
+
+    from oracle import fastmm_oracle as O
+
+    cores = min(16, os.cpu_count() or 1)
+    scheme = O.load_oracle_scheme(cfg["scheme"])
+    rows = 256
+    xs = x[:rows].float().numpy()
+    wn = w.float().numpy()
+    bn = None if b is None else b.float().numpy()
+    with threadpool_limits(limits=cores):
+        blas_threads = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
+        packed = O.weight_transform(scheme, wn) if cfg["prepacked"] else None
+
+        def one() -> None:
+            a = O.left_transform(scheme, xs)
+            bt = packed if packed is not None else O.weight_transform(scheme, wn)
+            p = O.leaf_products(a, bt, product_dtype="fp16", accumulate="f32")
+            O.reconstruct(scheme, p, rows, wn.shape[0], bn, "bf16")
+
+        one()  # warm
+        times = []
+        deadline = time.perf_counter() + budget_s
+        while True:
+            t0 = time.perf_counter()
+            one()
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() > deadline or len(times) >= 20:
+                break
+    seconds = float(np.median(times))
+    flops = 2.0 * rows * cfg["inner"] * cfg["columns"]
+    return {
+        "value": flops / seconds / 1e12,
+        "unit": "TFLOP/s",
+        "cores": int(min(cores, blas_threads)),
+        "kind": "port",
+        "sample": (
+            f"{rows} of {cfg['rows']} rows ({cfg['scheme']}, "
+            f"{'prepacked weight' if cfg['prepacked'] else 'weight transformed per call'}), "
+            f"fp32 BLAS leaf sums, median of {len(times)} runs, {seconds * 1e3:.0f} ms each"
+        ),
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser()
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    parser.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
+    parser.add_argument("--no-cpu", action="store_true")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: every box in this setup has one MI355X, and the "
+              "fast-matmul Linear path is single-GPU (row/column sharding needs no collective).",
+              file=sys.stderr)
+        return 2
+
+    from rdna3_fastmm.runtime import PLAN_TYPES
+
+    cfg = CONFIGS[args.config]
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    x_cpu, w_cpu, b_cpu = _inputs(cfg)
+    x, w = x_cpu.to(device), w_cpu.to(device)
+    b = None if b_cpu is None else b_cpu.to(device)
+    m, k, n = cfg["rows"], cfg["inner"], cfg["columns"]
+    flops = 2.0 * m * n * k
+
+    plan = PLAN_TYPES[cfg["scheme"]](m, k, n, device, dtype=torch.bfloat16, compute_dtype=torch.float16)
+    workspace = plan.allocate_workspace(prepacked_right=cfg["prepacked"])
+    packed = plan.pack_weight(w) if cfg["prepacked"] else None
+    out = torch.empty((m, n), device=device, dtype=torch.bfloat16) if cfg["prepacked"] else None
+    native_out = torch.empty((m, n), device=device, dtype=torch.bfloat16)
+
+    if cfg["prepacked"]:
+        def step():
+            plan.run_linear_packed(x, packed, workspace, b, out)
+
+        def native():
+            torch.mm(x, w.T, out=native_out)
+            if b is not None:
+                native_out.add_(b)
+    else:
+        def step():
+            plan.run_linear(x, w, workspace, b)
+
+        def native():
+            torch.nn.functional.linear(x, w, b)
+
+    for _ in range(args.warmup):
+        step()
+        native()
+    ms = _time_region(step, args.steps)
+    native_ms = _time_region(native, args.steps)
+
+    # Per-stage HIP-event timing (same stream as the launches).
+    shape = plan.shape
+    stages = {
+        "left_transform": lambda: plan._transform_left(x, workspace.left_transformed),
+        "leaf_products": lambda: plan._leaf_products(
+            workspace.left_transformed,
+            packed.transformed if packed is not None else workspace.right_transformed,
+            workspace.products,
+        ),
+        "reconstruct": lambda: plan._reconstruct(workspace.products, b, native_out),
+    }
+    if not cfg["prepacked"]:
+        stages["weight_transform"] = lambda: plan._transform_weight(w, workspace.right_transformed)
+    stage_ms = {name: _median(_event_ms(fn, 10)) for name, fn in stages.items()}
+    leaf_flops = 2.0 * plan.rank * shape.block_rows * shape.block_inner * shape.block_columns
+    leaf_tflops = leaf_flops / (stage_ms["leaf_products"] * 1e-3) / 1e12
+    pack_ms = _median(_event_ms(lambda: plan._transform_weight(w, workspace.products.new_empty(
+        (plan.rank, shape.block_columns, shape.block_inner))), 3))
+
+    # Accuracy on this workload (outside the timed region).
+    if cfg["prepacked"]:
+        result = plan.run_linear_packed(x, packed, workspace, b, out).clone()
+    else:
+        result = plan.run_linear(x, w, workspace, b)
+    exact = x.double() @ w.double().T
+    if b is not None:
+        exact += b.double()
+    norm = torch.linalg.vector_norm(exact)
+    native()
+    native_err = float(torch.linalg.vector_norm(native_out.double() - exact) / norm) if cfg["prepacked"] else float(
+        torch.linalg.vector_norm(torch.nn.functional.linear(x, w, b).double() - exact) / norm)
+    err = float(torch.linalg.vector_norm(result.double() - exact) / norm)
+    nonfinite = int((~torch.isfinite(result)).sum())
+    del exact
+
+    line = {
+        "metric": METRIC,
+        "value": round(flops / (ms * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 in/out, fp16 MFMA leaves, fp32 accumulate",
+        "data": "synthetic (seeded CPU torch.Generator: x~N(0,1), W~N(0,1/K), bias~N(0,0.02))",
+        "config": {
+            "workload": cfg["name"],
+            "scheme": cfg["scheme"],
+            "rows": m,
+            "inner": k,
+            "columns": n,
+            "bias": cfg["bias"],
+            "prepacked_weight": cfg["prepacked"],
+            "parallelism": "single GPU",
+        },
+        "native_bf16": {
+            "ms_per_step": round(native_ms, 4),
+            "tflops": round(flops / (native_ms * 1e-3) / 1e12, 2),
+            "op": "torch.mm(out=)+bias" if cfg["prepacked"] else "torch.nn.functional.linear",
+            "blas": str(torch.backends.cuda.preferred_blas_library()),
+            "TORCH_BLAS_PREFER_HIPBLASLT": os.environ.get("TORCH_BLAS_PREFER_HIPBLASLT"),
+        },
+        "speedup_vs_native": round(native_ms / ms, 4),
+        "accuracy": {
+            "rel_l2": err,
+            "native_rel_l2": native_err,
+            "error_ratio": round(err / native_err, 4),
+            "bound": 1.2,
+            "nonfinite": nonfinite,
+        },
+        "stages_ms": {name: round(v, 4) for name, v in stage_ms.items()},
+        "packing_ms": round(pack_ms, 4),
+        "roofline": {
+            "kernel": "leaf_gemm_kernel (fastmm_leaf_products)",
+            "bound": "mfma",
+            "achieved": round(leaf_tflops, 2),
+            "peak": MFMA_FP16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(leaf_tflops / MFMA_FP16_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "work_per_launch": f"2*R*Mb*Kb*Nb = {leaf_flops:.4e} flop",
+        },
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(cfg, x_cpu, w_cpu, b_cpu, args.cpu_budget)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

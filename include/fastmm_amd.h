@@ -1,0 +1,106 @@
+/*
+ * fastmm_amd.h -- C ABI of the MI355X (gfx950) fast-matmul Linear backend.
+ *
+ * The reference (chelokot/rdna3-fastmm) is Python + Triton and has no FFI of
+ * its own: its plan methods launch one Triton kernel (or one torch.bmm) per
+ * stage. Each entry point below replaces exactly one of those launches, with
+ * the same meaning, so the Python host layer (rdna3_fastmm.runtime / .linear)
+ * can keep the reference's plan and operator API and call these instead.
+ * Reference citations are paths in the reference repository.
+ *
+ * Conventions for every entry point:
+ *   - all pointers are device pointers on the current HIP device, contiguous,
+ *     row-major, and must not overlap (the host layer checks this);
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream); work is
+ *     enqueued asynchronously, nothing synchronizes;
+ *   - returns FASTMM_OK or an error code; fastmm_last_error() then describes
+ *     the failure (thread-local). Argument errors are reported before any
+ *     launch, so a failed call leaves every buffer untouched;
+ *   - block sizes follow the scheme's partition: with s = scheme size,
+ *     Mb = ceil(rows/s), Kb = ceil(inner/s), Nb = ceil(columns/s)
+ *     (runtime.py:66-78); rows/columns past the matrix read as zero.
+ *
+ * Layouts:
+ *   x / input      [rows, inner]            dtype (bf16 or fp16)
+ *   weight         [columns, inner]         dtype  (F.linear layout)
+ *   right          [inner, columns]         dtype  (mm path)
+ *   left_transformed  A'[R, Mb, Kb]         fp16
+ *   right_transformed B'[R, Nb, Kb]         fp16   (K-contiguous; the
+ *        reference stores [R, Kb, Nb] and transposes inside torch.bmm)
+ *   products       P[R, Mb, Nb]             fp16 or fp32
+ *   bias           [columns]                dtype
+ *   output         [rows, columns]          dtype
+ */
+#ifndef FASTMM_AMD_H
+#define FASTMM_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FASTMM_ABI_VERSION 1
+
+#define FASTMM_OK 0
+#define FASTMM_ERROR_ARGUMENT 1    /* bad pointer, size, dtype or scheme */
+#define FASTMM_ERROR_UNSUPPORTED 2 /* valid request this build does not run */
+#define FASTMM_ERROR_LAUNCH 3      /* the HIP runtime rejected a launch */
+
+#define FASTMM_BF16 0
+#define FASTMM_FP16 1
+#define FASTMM_FP32 2
+
+#define FASTMM_SCHEME_RANK7 0  /* <2,2,2> rank 7  (certificate 2x2x2_rank7_15add) */
+#define FASTMM_SCHEME_RANK48 1 /* <4,4,4> rank 48 (certificate 4x4x4_rank48_accurate) */
+#define FASTMM_SCHEME_RANK49 2 /* <4,4,4> rank 49 (certificate 4x4x4_rank49_159add) */
+
+/* Library identity. */
+int fastmm_abi_version(void);
+const char* fastmm_last_error(void);
+
+/* Scheme metadata compiled into the kernels; the host layer compares the
+ * digest with the certificate it verified, as the reference checks its
+ * generated modules at import (runtime.py:16-53). Returns FASTMM_OK or
+ * FASTMM_ERROR_ARGUMENT. */
+int fastmm_scheme_info(int scheme, int* size, int* rank);
+const char* fastmm_scheme_sha256(int scheme);
+
+/* A-side transform x[rows, inner] -> A'[R, Mb, Kb] fp16.
+ * Replaces _LinearPlan._transform_left + left_transform_kernel
+ * (runtime.py:597-615; generated/rank7_2x2x2.py:9-62). */
+int fastmm_left_transform(int scheme, int dtype, const void* input, void* left_transformed,
+                          int64_t rows, int64_t inner, void* stream);
+
+/* Weight transform W[columns, inner] -> B'[R, Nb, Kb] fp16 (prepack and the
+ * dynamic path). Replaces _LinearPlan._transform_weight +
+ * right_transform_weight_kernel (runtime.py:637-655; rank7_2x2x2.py:121-204). */
+int fastmm_weight_transform(int scheme, int dtype, const void* weight, void* right_transformed,
+                            int64_t columns, int64_t inner, void* stream);
+
+/* Right transform right[inner, columns] -> B'[R, Nb, Kb] fp16 (mm path).
+ * Replaces _LinearPlan._transform_right + right_transform_kernel
+ * (runtime.py:617-635; rank7_2x2x2.py:65-118). */
+int fastmm_right_transform(int scheme, int dtype, const void* right, void* right_transformed,
+                           int64_t inner, int64_t columns, void* stream);
+
+/* Leaf products P[r] = A'[r] @ B'[r]^T for r < rank, fp32 accumulation on
+ * FP16 MFMA, stored as products_dtype (FASTMM_FP16 = the reference's
+ * rounding, FASTMM_FP32 = no product rounding).
+ * Replaces torch.bmm(A', B', out=P) (runtime.py:728-732, 768-772). */
+int fastmm_leaf_products(int rank, const void* left_transformed, const void* right_transformed,
+                         void* products, int products_dtype, int64_t block_rows,
+                         int64_t block_inner, int64_t block_columns, void* stream);
+
+/* Output recombination P[R, Mb, Nb] -> output[rows, columns] in dtype, with
+ * an optional bias[columns] (NULL = none) added in fp32 after the scheme's
+ * sum. Replaces _reconstruct / _reconstruct_bias + output_transform[_bias]_kernel
+ * (runtime.py:657-698; rank7_2x2x2.py:207-345). */
+int fastmm_reconstruct(int scheme, int products_dtype, const void* products, const void* bias,
+                       int dtype, void* output, int64_t rows, int64_t columns, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FASTMM_AMD_H */

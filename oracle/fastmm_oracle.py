@@ -1,0 +1,392 @@
+"""CPU restatement of the reference's scheme evaluation (TEST INFRASTRUCTURE).
+
+This module is the parity oracle for the F.linear fast-matmul path. It is
+imported only by ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py``, always as the checker; the product
+(``rdna3_fastmm``) never imports, links or runs anything here.
+
+It restates, in numpy, the stage order and rounding points of the reference
+(paths relative to the reference repository):
+
+* block partition ``Mb = ceil(M/s)`` etc.: ``src/rdna3_fastmm/runtime.py:66-78``;
+* A-side transform: every input block loaded as fp32 (zero past ``M``/``K``),
+  the left program evaluated in fp32, every output plane stored as fp16
+  (round to nearest even): ``generated/rank7_2x2x2.py:9-62`` and the emitter
+  ``tools/generate_triton_scheme.py:133-233``;
+* weight transform from row-major ``W[N, K]`` (block ``j`` of ``W^T``):
+  ``generated/rank7_2x2x2.py:121-204``, emitter ``generate_triton_scheme.py:
+  240-337``;
+* leaf products ``P[r] = A'[r] @ B'[r]`` with fp16 operands: ``runtime.py:
+  728-732, 768-772`` (``torch.bmm``; fp32 accumulation, fp16 result);
+* reconstruction in fp32, ``+ bias`` after the whole expression, stored as
+  the output dtype: ``generated/rank7_2x2x2.py:207-345``, emitter
+  ``generate_triton_scheme.py:190-232``; output numbering column-major for
+  reduced circuits (``generate_triton_scheme.py:194-195``), row-major for SLP
+  files (``tools/generate_slp_triton_scheme.py:54-62``);
+* certificate expansion: ``certificate.py:58-78`` (reduced circuits, gates
+  then outputs, signed sums left to right) and ``slp.py:105-262`` (SLP
+  expressions, parsed as Python expressions, ``/2`` and ``*2`` scalings).
+
+How each function is pinned (tests/test_oracle.py):
+
+* ``load_oracle_scheme`` / ``evaluate_program``: exact Brent identity over
+  Fractions; the reference's own counts and digests (tests/test_slp.py:17-55,
+  tests/test_fastmm_certificate.py:31-33 of the reference); the W-circuit
+  semantics check of tests/test_generate_triton_scheme.py:47-98.
+* ``linear`` / ``matmul`` end to end: the exact small-integer known answer
+  (reference tests/test_rdna3.py:406-430) for all three schemes, the fp64
+  closed form ``x @ W.T`` on random inputs, and a planted sign error that
+  both checks must catch.
+* ``round_to_bf16``: bit-equal to ``torch.Tensor.to(torch.bfloat16)`` over
+  random, tie, subnormal, overflow and NaN inputs.
+* ``leaf_products`` with ``accumulate="f64"``: brute force against a Python
+  ``Fraction`` sum on tiny shapes.
+"""
+
+from __future__ import annotations
+
+import ast
+from dataclasses import dataclass
+from fractions import Fraction
+import json
+from pathlib import Path
+from typing import Any, Sequence
+
+import numpy as np
+
+CERTIFICATE_ROOT = (
+    Path(__file__).resolve().parent.parent / "rdna3-fastmm_amd" / "rdna3_fastmm" / "certificates"
+)
+SCHEME_DIRECTORIES = {
+    "rank7": "2x2x2_rank7_15add",
+    "rank48": "4x4x4_rank48_accurate",
+    "rank49": "4x4x4_rank49_159add",
+}
+
+# An expression is ("sig", index) | ("add", a, b) | ("sub", a, b) | ("neg", a)
+# | ("mul", a, Fraction) | ("div", a, Fraction).
+Node = tuple
+
+
+@dataclass
+class OracleProgram:
+    input_count: int
+    assignments: list[tuple[int, Node]]  # (signal index, expression)
+    outputs: list[int]  # signal index of each output, in C-block / plane order
+
+
+@dataclass
+class OracleScheme:
+    size: int
+    rank: int
+    left: OracleProgram
+    right: OracleProgram
+    output: OracleProgram  # outputs renumbered to row-major C blocks
+
+
+# ---------------------------------------------------------------- loading
+
+
+def _signed_sum(terms: list[dict[str, int]]) -> Node:
+    """reference certificate.py:58-78: sum left to right, first term signed."""
+    node: Node | None = None
+    for term in terms:
+        leaf: Node = ("sig", term["index"])
+        if node is None:
+            node = leaf if term["value"] == 1 else ("neg", leaf)
+        else:
+            node = ("add" if term["value"] == 1 else "sub", node, leaf)
+    assert node is not None
+    return node
+
+
+def _reduced_side(input_count: int, gates: list, outputs: list) -> OracleProgram:
+    assignments = []
+    for g, terms in enumerate(gates):
+        assignments.append((input_count + g, _signed_sum(terms)))
+    base = input_count + len(gates)
+    out_signals = []
+    for o, terms in enumerate(outputs):
+        assignments.append((base + o, _signed_sum(terms)))
+        out_signals.append(base + o)
+    return OracleProgram(input_count, assignments, out_signals)
+
+
+def _slp_node(node: ast.AST, names: dict[str, int]) -> Node | Fraction:
+    """reference slp.py:105-193, on Python's own expression parser."""
+    if isinstance(node, ast.Name):
+        return ("sig", names[node.id])
+    if isinstance(node, ast.Constant):
+        return Fraction(node.value)
+    assert isinstance(node, ast.BinOp), ast.dump(node)
+    left = _slp_node(node.left, names)
+    right = _slp_node(node.right, names)
+    if isinstance(node.op, ast.Add):
+        return ("add", left, right)
+    if isinstance(node.op, ast.Sub):
+        return ("sub", left, right)
+    if isinstance(node.op, ast.Mult):
+        if isinstance(left, Fraction):
+            return ("mul", right, left)
+        return ("mul", left, right)
+    assert isinstance(node.op, ast.Div)
+    return ("div", left, right)
+
+
+def _slp_side(path: Path, input_count: int, output_count: int) -> OracleProgram:
+    names = {f"i{i}": i for i in range(input_count)}
+    assignments = []
+    outputs: dict[int, int] = {}
+    for line in path.read_text().splitlines():
+        line = line.strip()
+        if not line:
+            continue
+        target, source = line.rstrip(";").split(":=")
+        node = _slp_node(ast.parse(source, mode="eval").body, names)
+        signal = input_count + len(assignments)
+        assignments.append((signal, node))
+        names[target] = signal
+        if target.startswith("o") and target[1:].isdigit():
+            outputs[int(target[1:])] = signal
+    return OracleProgram(input_count, assignments, [outputs[k] for k in range(output_count)])
+
+
+def load_oracle_scheme(key: str, root: Path = CERTIFICATE_ROOT) -> OracleScheme:
+    manifest_path = root / SCHEME_DIRECTORIES[key] / "certificate.json"
+    manifest = json.loads(manifest_path.read_text())
+    s, _, _ = manifest["n"]
+    rank = manifest["m"]
+    if "programs" in manifest:
+        directory = manifest_path.parent
+        left = _slp_side(directory / manifest["programs"]["u"], s * s, rank)
+        right = _slp_side(directory / manifest["programs"]["v"], s * s, rank)
+        output = _slp_side(directory / manifest["programs"]["w"], rank, s * s)
+        # SLP outputs are already row-major C blocks.
+    else:
+        left = _reduced_side(s * s, manifest["u_fresh"], manifest["u"])
+        right = _reduced_side(s * s, manifest["v_fresh"], manifest["v"])
+        output = _reduced_side(rank, manifest["w_fresh"], manifest["w"])
+        # Reduced outputs are column-major: output o is C block (o % s, o // s).
+        column_major = output.outputs
+        output.outputs = [column_major[col * s + row] for row in range(s) for col in range(s)]
+    return OracleScheme(s, rank, left, right, output)
+
+
+# ------------------------------------------------------------- evaluation
+
+
+def _eval(node: Node, values: dict[int, Any], scale_type: Any) -> Any:
+    kind = node[0]
+    if kind == "sig":
+        return values[node[1]]
+    if kind == "add":
+        a = _eval(node[1], values, scale_type)
+        return a + _eval(node[2], values, scale_type)
+    if kind == "sub":
+        a = _eval(node[1], values, scale_type)
+        return a - _eval(node[2], values, scale_type)
+    if kind == "neg":
+        return -_eval(node[1], values, scale_type)
+    operand = _eval(node[1], values, scale_type)
+    factor = node[2]
+    if kind == "mul":
+        return operand * scale_type(factor)
+    return operand / scale_type(factor)
+
+
+def evaluate_program(program: OracleProgram, inputs: Sequence[Any], scale_type: Any = np.float32) -> list:
+    """Evaluate every assignment in certificate order, each node rounded once.
+
+    ``scale_type`` turns a Fraction constant into the arithmetic type
+    (``np.float32`` for the fp32 kernels, ``Fraction`` for exact checks,
+    ``np.float64`` for the closed-form check).
+    """
+    values: dict[int, Any] = {i: inputs[i] for i in range(program.input_count)}
+    for signal, node in program.assignments:
+        values[signal] = _eval(node, values, scale_type)
+    return [values[signal] for signal in program.outputs]
+
+
+def program_matrix(program: OracleProgram) -> list[list[Fraction]]:
+    """Exact ``outputs x inputs`` coefficient matrix (symbolic evaluation)."""
+    n = program.input_count
+    unit = [np.array([Fraction(int(i == j)) for j in range(n)], dtype=object) for i in range(n)]
+    outputs = evaluate_program(program, unit, Fraction)
+    return [list(row) for row in outputs]
+
+
+# ---------------------------------------------------------------- rounding
+
+
+def round_to_bf16(values: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bits (uint16), round to nearest even; NaN -> quiet NaN."""
+    bits = np.ascontiguousarray(values, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    rounded = ((bits + 0x7FFF + ((bits >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = np.isnan(np.asarray(values, dtype=np.float32))
+    rounded[nan] = ((bits[nan] >> 16) | 0x40).astype(np.uint16)
+    return rounded
+
+
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def ceil_div(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+# ------------------------------------------------------------------ stages
+
+
+def _blocks(source: np.ndarray, s: int, rows_b: int, cols_b: int, transpose: bool) -> list[np.ndarray]:
+    """fp32 views of the s*s zero-padded blocks, row-major block order.
+
+    ``transpose=True`` reads block ``j`` of ``source^T`` (the weight layout:
+    ``source`` is ``W[N, K]``, block ``j`` is ``W^T`` block ``(j // s, j % s)``),
+    returned as an ``[Nb, Kb]`` array so the plane layout is K-contiguous.
+    """
+    rows, cols = source.shape
+    padded = np.zeros((rows_b * s, cols_b * s), dtype=np.float32)
+    padded[:rows, :cols] = source
+    blocks = []
+    for j in range(s * s):
+        br, bc = divmod(j, s)
+        if transpose:
+            # W^T block (br, bc) = W block (bc, br) transposed; keep it [Nb, Kb].
+            blocks.append(padded[bc * rows_b:(bc + 1) * rows_b, br * cols_b:(br + 1) * cols_b])
+        else:
+            blocks.append(padded[br * rows_b:(br + 1) * rows_b, bc * cols_b:(bc + 1) * cols_b])
+    return blocks
+
+
+def left_transform(scheme: OracleScheme, x: np.ndarray) -> np.ndarray:
+    """x[M, K] (values exact in fp32) -> A'[R, Mb, Kb] fp16."""
+    M, K = x.shape
+    s = scheme.size
+    planes = evaluate_program(scheme.left, _blocks(x, s, ceil_div(M, s), ceil_div(K, s), False))
+    return np.stack([np.asarray(p, dtype=np.float32) for p in planes]).astype(np.float16)
+
+
+def weight_transform(scheme: OracleScheme, weight: np.ndarray) -> np.ndarray:
+    """W[N, K] -> B'[R, Nb, Kb] fp16 (plane r is (sum_j V[r,j] W^T_j)^T)."""
+    N, K = weight.shape
+    s = scheme.size
+    planes = evaluate_program(scheme.right, _blocks(weight, s, ceil_div(N, s), ceil_div(K, s), True))
+    return np.stack([np.asarray(p, dtype=np.float32) for p in planes]).astype(np.float16)
+
+
+def right_transform(scheme: OracleScheme, right: np.ndarray) -> np.ndarray:
+    """right[K, N] (the mm path) -> B'[R, Nb, Kb] fp16, same planes as the weight path."""
+    return weight_transform(scheme, np.ascontiguousarray(right.T))
+
+
+def leaf_products(a: np.ndarray, b: np.ndarray, product_dtype: str = "fp16", accumulate: str = "f64") -> np.ndarray:
+    """P[r] = A'[r] @ B'[r]^T from fp16 planes.
+
+    ``accumulate="f64"`` is the near-exact sum (the parity reference; every
+    fp16 x fp16 product is exact in fp32 and the fp64 sum rounds once);
+    ``"f32"`` is an fp32 BLAS sum (the CPU baseline). ``product_dtype`` is
+    ``"fp16"`` (the reference's ``torch.bmm`` output) or ``"fp32"``.
+    """
+    work = np.float64 if accumulate == "f64" else np.float32
+    products = np.matmul(a.astype(work), np.swapaxes(b.astype(work), 1, 2))
+    if product_dtype == "fp16":
+        return products.astype(np.float16)
+    return products.astype(np.float32)
+
+
+def reconstruct(
+    scheme: OracleScheme,
+    products: np.ndarray,
+    rows: int,
+    columns: int,
+    bias: np.ndarray | None = None,
+    out_dtype: str = "bf16",
+) -> np.ndarray:
+    """C[M, N] from P[R, Mb, Nb]: fp32 program, ``+ bias`` last, then the output cast.
+
+    Returns bf16 bits (uint16) for ``out_dtype="bf16"``, fp16 values for
+    ``"fp16"``, fp32 values for ``"fp32"``.
+    """
+    s = scheme.size
+    _, mb, nb = products.shape
+    planes = [products[r].astype(np.float32) for r in range(scheme.rank)]
+    blocks = evaluate_program(scheme.output, planes)
+    full = np.zeros((mb * s, nb * s), dtype=np.float32)
+    padded_bias = None
+    if bias is not None:
+        padded_bias = np.zeros(nb * s, dtype=np.float32)
+        padded_bias[:columns] = bias
+    for c, block in enumerate(blocks):
+        br, bc = divmod(c, s)
+        value = np.asarray(block, dtype=np.float32)
+        if padded_bias is not None:
+            value = value + padded_bias[bc * nb:(bc + 1) * nb][None, :]
+        full[br * mb:(br + 1) * mb, bc * nb:(bc + 1) * nb] = value
+    result = full[:rows, :columns]
+    if out_dtype == "bf16":
+        return round_to_bf16(result)
+    if out_dtype == "fp16":
+        return result.astype(np.float16)
+    return result
+
+
+def linear(
+    scheme: OracleScheme,
+    x: np.ndarray,
+    weight: np.ndarray,
+    bias: np.ndarray | None = None,
+    product_dtype: str = "fp16",
+    accumulate: str = "f64",
+    out_dtype: str = "bf16",
+) -> np.ndarray:
+    """F.linear(x, W, bias) through the scheme, reference stage order."""
+    a = left_transform(scheme, x)
+    b = weight_transform(scheme, weight)
+    p = leaf_products(a, b, product_dtype, accumulate)
+    return reconstruct(scheme, p, x.shape[0], weight.shape[0], bias, out_dtype)
+
+
+def matmul(
+    scheme: OracleScheme,
+    left: np.ndarray,
+    right: np.ndarray,
+    product_dtype: str = "fp16",
+    accumulate: str = "f64",
+    out_dtype: str = "fp16",
+) -> np.ndarray:
+    """left[M, K] @ right[K, N] through the scheme (the plan ``run`` path)."""
+    a = left_transform(scheme, left)
+    b = right_transform(scheme, right)
+    p = leaf_products(a, b, product_dtype, accumulate)
+    return reconstruct(scheme, p, left.shape[0], right.shape[1], None, out_dtype)
+
+
+def linear_float64(scheme: OracleScheme, x: np.ndarray, weight: np.ndarray) -> np.ndarray:
+    """Every stage in fp64 with no intermediate rounding: must equal x @ W^T."""
+    s = scheme.size
+    M, K = x.shape
+    N = weight.shape[0]
+    mb, kb, nb = ceil_div(M, s), ceil_div(K, s), ceil_div(N, s)
+
+    def blocks(src: np.ndarray, rb: int, cb: int, transpose: bool) -> list[np.ndarray]:
+        padded = np.zeros((rb * s, cb * s))
+        padded[: src.shape[0], : src.shape[1]] = src
+        out = []
+        for j in range(s * s):
+            br, bc = divmod(j, s)
+            if transpose:
+                out.append(padded[bc * rb:(bc + 1) * rb, br * cb:(br + 1) * cb])
+            else:
+                out.append(padded[br * rb:(br + 1) * rb, bc * cb:(bc + 1) * cb])
+        return out
+
+    a = evaluate_program(scheme.left, blocks(x, mb, kb, False), np.float64)
+    b = evaluate_program(scheme.right, blocks(weight, nb, kb, True), np.float64)
+    p = [np.asarray(a[r]) @ np.asarray(b[r]).T for r in range(scheme.rank)]
+    c = evaluate_program(scheme.output, p, np.float64)
+    full = np.zeros((mb * s, nb * s))
+    for q, block in enumerate(c):
+        br, bc = divmod(q, s)
+        full[br * mb:(br + 1) * mb, bc * nb:(bc + 1) * nb] = block
+    return full[:M, :N]

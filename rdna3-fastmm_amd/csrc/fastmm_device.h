@@ -1,0 +1,137 @@
+// Device-side building blocks shared by the fast-matmul kernels (gfx950).
+#ifndef FASTMM_DEVICE_H
+#define FASTMM_DEVICE_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fastmm {
+
+typedef _Float16 half_t;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+
+// Element codes shared with the C ABI (include/fastmm_amd.h).
+enum DType : int { kBF16 = 0, kFP16 = 1, kFP32 = 2 };
+
+// ---------------------------------------------------------------- scalars
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t bits) {
+  return __uint_as_float(static_cast<uint32_t>(bits) << 16);
+}
+
+// fp32 -> bf16, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16(float value) {
+  uint32_t bits = __float_as_uint(value);
+  if ((bits & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((bits >> 16) | 0x40u);
+  bits += 0x7fffu + ((bits >> 16) & 1u);
+  return static_cast<uint16_t>(bits >> 16);
+}
+
+__device__ __forceinline__ float fp16_to_f32(uint16_t bits) {
+  return static_cast<float>(__builtin_bit_cast(half_t, bits));
+}
+
+// fp32 -> fp16 with the hardware conversion (round to nearest even).
+__device__ __forceinline__ uint16_t f32_to_fp16(float value) {
+  return __builtin_bit_cast(uint16_t, static_cast<half_t>(value));
+}
+
+template <int kDType>
+__device__ __forceinline__ float to_f32(uint16_t bits) {
+  if constexpr (kDType == kBF16) return bf16_to_f32(bits);
+  else return fp16_to_f32(bits);
+}
+
+template <int kDType>
+__device__ __forceinline__ uint16_t from_f32(float value) {
+  if constexpr (kDType == kBF16) return f32_to_bf16(value);
+  else return f32_to_fp16(value);
+}
+
+// ------------------------------------------------------------ value vector
+
+// N consecutive fp32 values; every operator rounds once per element, so a
+// straight-line program evaluated on Vec<N> rounds exactly as on float.
+template <int N>
+struct Vec {
+  float v[N];
+
+  __device__ __forceinline__ Vec operator+(const Vec& o) const {
+    Vec r;
+#pragma unroll
+    for (int i = 0; i < N; ++i) r.v[i] = v[i] + o.v[i];
+    return r;
+  }
+  __device__ __forceinline__ Vec operator-(const Vec& o) const {
+    Vec r;
+#pragma unroll
+    for (int i = 0; i < N; ++i) r.v[i] = v[i] - o.v[i];
+    return r;
+  }
+  __device__ __forceinline__ Vec operator-() const {
+    Vec r;
+#pragma unroll
+    for (int i = 0; i < N; ++i) r.v[i] = -v[i];
+    return r;
+  }
+  __device__ __forceinline__ Vec operator*(float k) const {
+    Vec r;
+#pragma unroll
+    for (int i = 0; i < N; ++i) r.v[i] = v[i] * k;
+    return r;
+  }
+  __device__ __forceinline__ static Vec zero() {
+    Vec r;
+#pragma unroll
+    for (int i = 0; i < N; ++i) r.v[i] = 0.0f;
+    return r;
+  }
+};
+
+// ------------------------------------------------- 16-bit vector memory ops
+
+// N 16-bit elements as one 2/4/8/16-byte access (N = 1, 2, 4, 8).
+template <int N> struct Raw16;
+template <> struct Raw16<1> { typedef uint16_t type; };
+template <> struct Raw16<2> { typedef uint32_t type; };
+template <> struct Raw16<4> { typedef uint2 type; };
+template <> struct Raw16<8> { typedef uint4 type; };
+
+template <int N>
+__device__ __forceinline__ void load16(const uint16_t* p, uint16_t (&out)[N]) {
+  typedef typename Raw16<N>::type R;
+  const R raw = *reinterpret_cast<const R*>(p);
+  __builtin_memcpy(out, &raw, sizeof(R));
+}
+
+template <int N>
+__device__ __forceinline__ void store16(uint16_t* p, const uint16_t (&in)[N]) {
+  typedef typename Raw16<N>::type R;
+  R raw;
+  __builtin_memcpy(&raw, in, sizeof(R));
+  *reinterpret_cast<R*>(p) = raw;
+}
+
+template <int kDType, int N>
+__device__ __forceinline__ Vec<N> load_vec(const uint16_t* p) {
+  uint16_t raw[N];
+  load16<N>(p, raw);
+  Vec<N> r;
+#pragma unroll
+  for (int i = 0; i < N; ++i) r.v[i] = to_f32<kDType>(raw[i]);
+  return r;
+}
+
+template <int kDType, int N>
+__device__ __forceinline__ void store_vec(uint16_t* p, const Vec<N>& value) {
+  uint16_t raw[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) raw[i] = from_f32<kDType>(value.v[i]);
+  store16<N>(p, raw);
+}
+
+}  // namespace fastmm
+
+#endif  // FASTMM_DEVICE_H

@@ -1,0 +1,396 @@
+// Block transforms and output recombination for every scheme (gfx950).
+//
+// All three kernels are HBM-bound elementwise passes over one block plane:
+// a thread owns EPT consecutive plane elements (K-contiguous for the
+// transforms, N-contiguous for the recombination), reads the s*s input
+// blocks (or the R products) at that position with 8/16-byte vector loads,
+// evaluates the scheme's straight-line program in fp32 registers, and writes
+// every output with one vector store as soon as the program produces it.
+// Positions past the matrix read as zero (the reference's masked loads with
+// other=0.0). Programs come from csrc/generated/*.h.
+#include "abi_common.h"
+#include "fastmm_device.h"
+#include "generated/rank48_4x4x4.h"
+#include "generated/rank49_4x4x4.h"
+#include "generated/rank7_2x2x2.h"
+
+namespace fastmm {
+
+constexpr int kThreads = 256;
+
+// Elements per thread of the vector path: 8 (16-byte accesses) for the small
+// rank-7 program; 4 for the 48/49-output programs, whose live fp32 values
+// would otherwise spill.
+template <class S>
+constexpr int vector_width() { return S::kRank <= 8 ? 8 : 4; }
+
+enum Side : int { kLeftSide = 0, kWeightSide = 1 };
+
+// A' = left(x blocks) or B' = right(W^T blocks), read K-contiguous.
+// Left:   input j = x block (j / s, j % s)      over x[src_rows, src_cols].
+// Weight: input j = W^T block (j / s, j % s) = W block (j % s, j / s) over
+//         W[src_rows = N, src_cols = K]; plane r of B' is [Nb, Kb].
+// kVector: src_cols == s * cols_b, cols_b % EPT == 0 and 2*EPT-aligned
+// pointers, so every vector is wholly inside a row; otherwise EPT == 1.
+template <class S, int kSide, int kDType, int EPT, bool kVector>
+__global__ __launch_bounds__(kThreads) void direct_transform_kernel(
+    const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, int64_t src_rows,
+    int64_t src_cols, int64_t rows_b, int64_t cols_b) {
+  constexpr int s = S::kSize;
+  const int64_t plane = rows_b * cols_b;
+  const int64_t first = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * EPT;
+  if (first >= plane) return;
+  const int64_t row = first / cols_b;
+  const int64_t col = first - row * cols_b;
+
+  auto load = [&](int j) -> Vec<EPT> {
+    const int block_row = kSide == kLeftSide ? j / s : j % s;
+    const int block_col = kSide == kLeftSide ? j % s : j / s;
+    const int64_t r = block_row * rows_b + row;
+    const int64_t c = block_col * cols_b + col;
+    if (r >= src_rows) return Vec<EPT>::zero();
+    if constexpr (kVector) {
+      return load_vec<kDType, EPT>(src + r * src_cols + c);
+    } else {
+      Vec<EPT> v;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        v.v[e] = (c + e < src_cols) ? to_f32<kDType>(src[r * src_cols + c + e]) : 0.0f;
+      }
+      return v;
+    }
+  };
+  auto store = [&](int k, const Vec<EPT>& v) {
+    store_vec<kFP16, EPT>(dst + k * plane + first, v);
+  };
+  if constexpr (kSide == kLeftSide) {
+    S::template left<Vec<EPT>>(load, store);
+  } else {
+    S::template right<Vec<EPT>>(load, store);
+  }
+}
+
+// B' from a row-major right[K, N] (the mm path): the blocks are N-contiguous
+// in memory but B' planes are K-contiguous, so a 32x32 (k, n) tile of every
+// input block is staged through LDS and read transposed.
+constexpr int kTransposeTile = 32;
+
+template <class S, int kDType>
+__global__ __launch_bounds__(kThreads) void transposed_right_kernel(
+    const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, int64_t inner,
+    int64_t columns, int64_t kb, int64_t nb) {
+  constexpr int s = S::kSize;
+  constexpr int T = kTransposeTile;
+  __shared__ float tile[s * s][T][T + 1];
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * T;
+  const int64_t k0 = static_cast<int64_t>(blockIdx.y) * T;
+  const int tid = threadIdx.x;
+  const int nn = tid % T;
+#pragma unroll
+  for (int j = 0; j < s * s; ++j) {
+    const int64_t block_k = j / s, block_n = j % s;
+#pragma unroll
+    for (int pass = 0; pass < T * T / kThreads; ++pass) {
+      const int kk = tid / T + pass * (kThreads / T);
+      const int64_t k = k0 + kk, n = n0 + nn;
+      const int64_t src_row = block_k * kb + k, src_col = block_n * nb + n;
+      float value = 0.0f;
+      if (k < kb && n < nb && src_row < inner && src_col < columns) {
+        value = to_f32<kDType>(src[src_row * columns + src_col]);
+      }
+      tile[j][kk][nn] = value;
+    }
+  }
+  __syncthreads();
+  const int n_local = tid / 8;
+  const int k_local = (tid % 8) * 4;
+  auto load = [&](int j) -> Vec<4> {
+    Vec<4> v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v.v[e] = tile[j][k_local + e][n_local];
+    return v;
+  };
+  const int64_t n = n0 + n_local;
+  const int64_t k = k0 + k_local;
+  auto store = [&](int r, const Vec<4>& v) {
+    if (n >= nb) return;
+    uint16_t* p = dst + (static_cast<int64_t>(r) * nb + n) * kb + k;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (k + e < kb) p[e] = f32_to_fp16(v.v[e]);
+    }
+  };
+  S::template right<Vec<4>>(load, store);
+}
+
+// C = output(P planes) (+ bias), stored as kOut. One thread: EPT consecutive
+// columns of one product-plane row, i.e. the same EPT columns of s output
+// rows... of every output block at that position.
+template <int kProd, int EPT>
+__device__ __forceinline__ Vec<EPT> load_product(const void* products, int64_t offset) {
+  if constexpr (kProd == kFP32) {
+    const float* p = static_cast<const float*>(products) + offset;
+    Vec<EPT> v;
+    if constexpr (EPT % 4 == 0) {
+#pragma unroll
+      for (int e = 0; e < EPT; e += 4) {
+        const float4 q = *reinterpret_cast<const float4*>(p + e);
+        v.v[e] = q.x;
+        v.v[e + 1] = q.y;
+        v.v[e + 2] = q.z;
+        v.v[e + 3] = q.w;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) v.v[e] = p[e];
+    }
+    return v;
+  } else {
+    return load_vec<kFP16, EPT>(static_cast<const uint16_t*>(products) + offset);
+  }
+}
+
+template <class S, int kProd, int kOut, int EPT, bool kVector, bool kBias>
+__global__ __launch_bounds__(kThreads) void reconstruct_kernel(
+    const void* __restrict__ products, const uint16_t* __restrict__ bias,
+    uint16_t* __restrict__ out, int64_t rows, int64_t cols, int64_t rows_b, int64_t cols_b) {
+  constexpr int s = S::kSize;
+  const int64_t plane = rows_b * cols_b;
+  const int64_t first = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * EPT;
+  if (first >= plane) return;
+  const int64_t row = first / cols_b;
+  const int64_t col = first - row * cols_b;
+
+  auto load = [&](int r) -> Vec<EPT> {
+    return load_product<kProd, EPT>(products, static_cast<int64_t>(r) * plane + first);
+  };
+  auto store = [&](int c, Vec<EPT> v) {
+    const int64_t out_row = (c / s) * rows_b + row;
+    if (out_row >= rows) return;
+    const int64_t out_col = (c % s) * cols_b + col;
+    uint16_t* p = out + out_row * cols + out_col;
+    if constexpr (kVector) {
+      if constexpr (kBias) {
+        const Vec<EPT> b = load_vec<kOut, EPT>(bias + out_col);
+        v = v + b;
+      }
+      store_vec<kOut, EPT>(p, v);
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        if (out_col + e < cols) {
+          float value = v.v[e];
+          if constexpr (kBias) value = value + to_f32<kOut>(bias[out_col + e]);
+          p[e] = from_f32<kOut>(value);
+        }
+      }
+    }
+  };
+  S::template output<Vec<EPT>>(load, store);
+}
+
+// ------------------------------------------------------------- launchers
+
+template <class S>
+int launch_direct(int side, int dtype, const void* src, void* dst, int64_t src_rows,
+                  int64_t src_cols, hipStream_t stream) {
+  constexpr int s = S::kSize;
+  constexpr int W = vector_width<S>();
+  const int64_t rows_b = ceil_div(src_rows, s);
+  const int64_t cols_b = ceil_div(src_cols, s);
+  const bool vector = src_cols % (s * W) == 0 && aligned_to(src, 2 * W) && aligned_to(dst, 2 * W);
+  const int64_t plane = rows_b * cols_b;
+  const int64_t per_block = static_cast<int64_t>(kThreads) * (vector ? W : 1);
+  const dim3 grid(static_cast<unsigned>(ceil_div(plane, per_block)));
+  const uint16_t* in = static_cast<const uint16_t*>(src);
+  uint16_t* out = static_cast<uint16_t*>(dst);
+#define FASTMM_DIRECT(SIDE, DT)                                                              \
+  do {                                                                                       \
+    if (vector)                                                                              \
+      direct_transform_kernel<S, SIDE, DT, W, true>                                          \
+          <<<grid, kThreads, 0, stream>>>(in, out, src_rows, src_cols, rows_b, cols_b);      \
+    else                                                                                     \
+      direct_transform_kernel<S, SIDE, DT, 1, false>                                         \
+          <<<grid, kThreads, 0, stream>>>(in, out, src_rows, src_cols, rows_b, cols_b);      \
+  } while (0)
+  if (side == kLeftSide) {
+    if (dtype == kBF16) FASTMM_DIRECT(kLeftSide, kBF16);
+    else FASTMM_DIRECT(kLeftSide, kFP16);
+  } else {
+    if (dtype == kBF16) FASTMM_DIRECT(kWeightSide, kBF16);
+    else FASTMM_DIRECT(kWeightSide, kFP16);
+  }
+#undef FASTMM_DIRECT
+  return check_launch(side == kLeftSide ? "left transform" : "weight transform");
+}
+
+template <class S>
+int launch_transposed(int dtype, const void* src, void* dst, int64_t inner, int64_t columns,
+                      hipStream_t stream) {
+  constexpr int s = S::kSize;
+  const int64_t kb = ceil_div(inner, s);
+  const int64_t nb = ceil_div(columns, s);
+  const dim3 grid(static_cast<unsigned>(ceil_div(nb, kTransposeTile)),
+                  static_cast<unsigned>(ceil_div(kb, kTransposeTile)));
+  const uint16_t* in = static_cast<const uint16_t*>(src);
+  uint16_t* out = static_cast<uint16_t*>(dst);
+  if (dtype == kBF16) {
+    transposed_right_kernel<S, kBF16><<<grid, kThreads, 0, stream>>>(in, out, inner, columns, kb, nb);
+  } else {
+    transposed_right_kernel<S, kFP16><<<grid, kThreads, 0, stream>>>(in, out, inner, columns, kb, nb);
+  }
+  return check_launch("right transform");
+}
+
+template <class S, int kProd, int kOut, bool kBias>
+void launch_reconstruct_typed(bool vector, dim3 grid, hipStream_t stream, const void* products,
+                              const uint16_t* bias, uint16_t* out, int64_t rows, int64_t cols,
+                              int64_t rows_b, int64_t cols_b) {
+  constexpr int W = vector_width<S>();
+  if (vector) {
+    reconstruct_kernel<S, kProd, kOut, W, true, kBias>
+        <<<grid, kThreads, 0, stream>>>(products, bias, out, rows, cols, rows_b, cols_b);
+  } else {
+    reconstruct_kernel<S, kProd, kOut, 1, false, kBias>
+        <<<grid, kThreads, 0, stream>>>(products, bias, out, rows, cols, rows_b, cols_b);
+  }
+}
+
+template <class S>
+int launch_reconstruct(int products_dtype, const void* products, const void* bias, int dtype,
+                       void* output, int64_t rows, int64_t cols, hipStream_t stream) {
+  constexpr int s = S::kSize;
+  constexpr int W = vector_width<S>();
+  const int64_t rows_b = ceil_div(rows, s);
+  const int64_t cols_b = ceil_div(cols, s);
+  const int product_bytes = products_dtype == kFP32 ? 4 : 2;
+  const bool vector = cols % (s * W) == 0 && aligned_to(products, product_bytes * W) &&
+                      aligned_to(output, 2 * W) && (bias == nullptr || aligned_to(bias, 2 * W));
+  const int64_t plane = rows_b * cols_b;
+  const int64_t per_block = static_cast<int64_t>(kThreads) * (vector ? W : 1);
+  const dim3 grid(static_cast<unsigned>(ceil_div(plane, per_block)));
+  const uint16_t* b = static_cast<const uint16_t*>(bias);
+  uint16_t* out = static_cast<uint16_t*>(output);
+#define FASTMM_RECON(PROD, OUT)                                                                 \
+  do {                                                                                          \
+    if (b)                                                                                      \
+      launch_reconstruct_typed<S, PROD, OUT, true>(vector, grid, stream, products, b, out,      \
+                                                   rows, cols, rows_b, cols_b);                 \
+    else                                                                                        \
+      launch_reconstruct_typed<S, PROD, OUT, false>(vector, grid, stream, products, b, out,     \
+                                                    rows, cols, rows_b, cols_b);                \
+  } while (0)
+  if (products_dtype == kFP32) {
+    if (dtype == kBF16) FASTMM_RECON(kFP32, kBF16);
+    else FASTMM_RECON(kFP32, kFP16);
+  } else {
+    if (dtype == kBF16) FASTMM_RECON(kFP16, kBF16);
+    else FASTMM_RECON(kFP16, kFP16);
+  }
+#undef FASTMM_RECON
+  return check_launch("reconstruct");
+}
+
+// Calls f.template operator()<Scheme>() for the scheme id, or fails.
+template <class F>
+int with_scheme(int scheme, F&& f) {
+  switch (scheme) {
+    case FASTMM_SCHEME_RANK7: return f.template operator()<SchemeRank7>();
+    case FASTMM_SCHEME_RANK48: return f.template operator()<SchemeRank48>();
+    case FASTMM_SCHEME_RANK49: return f.template operator()<SchemeRank49>();
+    default: return fail(FASTMM_ERROR_ARGUMENT, "unknown scheme id %d", scheme);
+  }
+}
+
+int check_io(const char* name, int dtype, const void* a, const void* b, int64_t rows,
+             int64_t cols) {
+  if (dtype != kBF16 && dtype != kFP16) {
+    return fail(FASTMM_ERROR_ARGUMENT, "%s: dtype must be bf16 or fp16, got %d", name, dtype);
+  }
+  if (a == nullptr || b == nullptr) return fail(FASTMM_ERROR_ARGUMENT, "%s: null pointer", name);
+  if (rows < 1 || cols < 1) {
+    return fail(FASTMM_ERROR_ARGUMENT, "%s: dimensions must be positive", name);
+  }
+  if (rows > (int64_t{1} << 31) || cols > (int64_t{1} << 31)) {
+    return fail(FASTMM_ERROR_UNSUPPORTED, "%s: dimension too large", name);
+  }
+  return FASTMM_OK;
+}
+
+}  // namespace fastmm
+
+using namespace fastmm;
+
+extern "C" int fastmm_scheme_info(int scheme, int* size, int* rank) {
+  clear_error();
+  return with_scheme(scheme, [&]<class S>() {
+    if (size) *size = S::kSize;
+    if (rank) *rank = S::kRank;
+    return FASTMM_OK;
+  });
+}
+
+extern "C" const char* fastmm_scheme_sha256(int scheme) {
+  switch (scheme) {
+    case FASTMM_SCHEME_RANK7: return SchemeRank7::kCertificateSha256;
+    case FASTMM_SCHEME_RANK48: return SchemeRank48::kCertificateSha256;
+    case FASTMM_SCHEME_RANK49: return SchemeRank49::kCertificateSha256;
+    default: return nullptr;
+  }
+}
+
+extern "C" int fastmm_left_transform(int scheme, int dtype, const void* input,
+                                     void* left_transformed, int64_t rows, int64_t inner,
+                                     void* stream) {
+  clear_error();
+  if (int status = check_io("left transform", dtype, input, left_transformed, rows, inner)) {
+    return status;
+  }
+  return with_scheme(scheme, [&]<class S>() {
+    return launch_direct<S>(kLeftSide, dtype, input, left_transformed, rows, inner,
+                            static_cast<hipStream_t>(stream));
+  });
+}
+
+extern "C" int fastmm_weight_transform(int scheme, int dtype, const void* weight,
+                                       void* right_transformed, int64_t columns, int64_t inner,
+                                       void* stream) {
+  clear_error();
+  if (int status =
+          check_io("weight transform", dtype, weight, right_transformed, columns, inner)) {
+    return status;
+  }
+  return with_scheme(scheme, [&]<class S>() {
+    return launch_direct<S>(kWeightSide, dtype, weight, right_transformed, columns, inner,
+                            static_cast<hipStream_t>(stream));
+  });
+}
+
+extern "C" int fastmm_right_transform(int scheme, int dtype, const void* right,
+                                      void* right_transformed, int64_t inner, int64_t columns,
+                                      void* stream) {
+  clear_error();
+  if (int status = check_io("right transform", dtype, right, right_transformed, inner, columns)) {
+    return status;
+  }
+  return with_scheme(scheme, [&]<class S>() {
+    return launch_transposed<S>(dtype, right, right_transformed, inner, columns,
+                                static_cast<hipStream_t>(stream));
+  });
+}
+
+extern "C" int fastmm_reconstruct(int scheme, int products_dtype, const void* products,
+                                  const void* bias, int dtype, void* output, int64_t rows,
+                                  int64_t columns, void* stream) {
+  clear_error();
+  if (int status = check_io("reconstruct", dtype, products, output, rows, columns)) {
+    return status;
+  }
+  if (products_dtype != kFP16 && products_dtype != kFP32) {
+    return fail(FASTMM_ERROR_ARGUMENT, "reconstruct: products must be fp16 or fp32");
+  }
+  return with_scheme(scheme, [&]<class S>() {
+    return launch_reconstruct<S>(products_dtype, products, bias, dtype, output, rows, columns,
+                                 static_cast<hipStream_t>(stream));
+  });
+}

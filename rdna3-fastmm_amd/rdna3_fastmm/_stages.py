@@ -1,0 +1,101 @@
+"""One function per HIP stage: tensors in, a launch on the current stream out.
+
+Shared by the plans (``runtime``) and the allocating operators (``linear``).
+Callers validate shapes, dtypes and storage; these only marshal pointers.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _native
+from .schemes import Scheme
+
+
+def left_transform(scheme: Scheme, source: torch.Tensor, output: torch.Tensor, rows: int, inner: int) -> None:
+    with torch.cuda.device(source.device):
+        _native.call(
+            "fastmm_left_transform",
+            scheme.scheme_id,
+            _native.dtype_code(source.dtype),
+            source.data_ptr(),
+            output.data_ptr(),
+            rows,
+            inner,
+            _native.stream_handle(source.device),
+        )
+
+
+def weight_transform(scheme: Scheme, weight: torch.Tensor, output: torch.Tensor, columns: int, inner: int) -> None:
+    with torch.cuda.device(weight.device):
+        _native.call(
+            "fastmm_weight_transform",
+            scheme.scheme_id,
+            _native.dtype_code(weight.dtype),
+            weight.data_ptr(),
+            output.data_ptr(),
+            columns,
+            inner,
+            _native.stream_handle(weight.device),
+        )
+
+
+def right_transform(scheme: Scheme, right: torch.Tensor, output: torch.Tensor, inner: int, columns: int) -> None:
+    with torch.cuda.device(right.device):
+        _native.call(
+            "fastmm_right_transform",
+            scheme.scheme_id,
+            _native.dtype_code(right.dtype),
+            right.data_ptr(),
+            output.data_ptr(),
+            inner,
+            columns,
+            _native.stream_handle(right.device),
+        )
+
+
+def leaf_products(
+    rank: int,
+    left: torch.Tensor,
+    right: torch.Tensor,
+    products: torch.Tensor,
+    block_rows: int,
+    block_inner: int,
+    block_columns: int,
+) -> None:
+    with torch.cuda.device(left.device):
+        _native.call(
+            "fastmm_leaf_products",
+            rank,
+            left.data_ptr(),
+            right.data_ptr(),
+            products.data_ptr(),
+            _native.dtype_code(products.dtype),
+            block_rows,
+            block_inner,
+            block_columns,
+            _native.stream_handle(left.device),
+        )
+
+
+def reconstruct(
+    scheme: Scheme,
+    products: torch.Tensor,
+    bias: torch.Tensor | None,
+    output: torch.Tensor,
+    rows: int,
+    columns: int,
+) -> None:
+    with torch.cuda.device(products.device):
+        _native.call(
+            "fastmm_reconstruct",
+            scheme.scheme_id,
+            _native.dtype_code(products.dtype),
+            products.data_ptr(),
+            None if bias is None else bias.data_ptr(),
+            _native.dtype_code(output.dtype),
+            output.data_ptr(),
+            rows,
+            columns,
+            _native.stream_handle(products.device),
+        )

@@ -1,0 +1,205 @@
+"""Allocating ``F.linear`` operators and the pre-AOT FX rewrite.
+
+``torch.ops.rdna3_fastmm.linear`` (rank 49) and
+``torch.ops.rdna3_fastmm.linear_rank7`` keep the reference's schemas
+(``src/rdna3_fastmm/linear.py:50-167``): functional, ``(Tensor input, Tensor
+weight, Tensor? bias=None) -> Tensor``, any number of leading dimensions,
+with a fake (meta) implementation so Dynamo/Inductor treat them as opaque
+extern kernels. The reference builds them as ``triton_op``s so Inductor can
+see the Triton kernels; these are ``torch.library.custom_op``s over the HIP
+library, which Inductor calls as a fallback kernel.
+
+``rewrite_eligible_linears`` replaces eligible ``aten.linear`` nodes of a
+graph before AOT compilation, exactly where the reference does
+(linear.py:170-288): BF16 input/weight/bias on one GPU, contiguous, static
+shape, a measured-win family (rank-7 families first, then rank-49), and at
+most half of the free device memory for the temporaries.
+"""
+
+from typing import Callable, Optional
+
+import torch
+from torch.fx import GraphModule, Node
+from torch.fx.passes.fake_tensor_prop import FakeTensorProp
+
+from . import _stages
+from .runtime import Rank7Plan, Rank48Plan, Rank49Plan, _check_library_scheme, _LinearPlan
+from .schemes import load_scheme
+
+LINEAR_TARGETS = frozenset({torch._C._nn.linear, torch.ops.aten.linear.default})
+MAX_LINEAR_ALLOCATION_FREE_FRACTION = 0.5
+
+
+def _ceil_div(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+def _check_operands(name: str, input_tensor: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor]) -> None:
+    if input_tensor.dtype not in (torch.bfloat16, torch.float16) or weight.dtype != input_tensor.dtype:
+        raise ValueError(f"{name} needs bf16 or fp16 input and weight of one dtype")
+    if input_tensor.device.type != "cuda" or weight.device != input_tensor.device:
+        raise ValueError(f"{name} needs input and weight on one ROCm device")
+    if weight.dim() != 2 or input_tensor.dim() < 1 or input_tensor.shape[-1] != weight.shape[1]:
+        raise ValueError(f"{name}: input [..., K] and weight [N, K] do not match")
+    if not input_tensor.is_contiguous() or not weight.is_contiguous():
+        raise ValueError(f"{name} needs contiguous input and weight")
+    if bias is not None and (
+        tuple(bias.shape) != (weight.shape[0],)
+        or bias.dtype != input_tensor.dtype
+        or bias.device != input_tensor.device
+        or not bias.is_contiguous()
+    ):
+        raise ValueError(f"{name}: bias must be a contiguous [N] tensor of the input dtype")
+
+
+def _linear(plan_type: type, name: str, input_tensor: torch.Tensor, weight: torch.Tensor,
+            bias: Optional[torch.Tensor]) -> torch.Tensor:
+    """One dynamic linear through the scheme; temporaries freed before the output exists.
+
+    Stage order and the early release of A'/B' follow reference linear.py:66-153.
+    """
+    _check_operands(name, input_tensor, weight, bias)
+    scheme = load_scheme(plan_type.scheme_key)
+    _check_library_scheme(scheme)
+    inner = input_tensor.shape[-1]
+    columns = weight.shape[0]
+    flat = input_tensor.reshape(-1, inner)
+    rows = flat.shape[0]
+    s, rank = scheme.size, scheme.rank
+    mb, kb, nb = _ceil_div(rows, s), _ceil_div(inner, s), _ceil_div(columns, s)
+    device = input_tensor.device
+    left = torch.empty((rank, mb, kb), device=device, dtype=torch.float16)
+    right = torch.empty((rank, nb, kb), device=device, dtype=torch.float16)
+    _stages.left_transform(scheme, flat, left, rows, inner)
+    _stages.weight_transform(scheme, weight, right, columns, inner)
+    products = torch.empty((rank, mb, nb), device=device, dtype=torch.float16)
+    _stages.leaf_products(rank, left, right, products, mb, kb, nb)
+    del left, right
+    output = torch.empty((rows, columns), device=device, dtype=input_tensor.dtype)
+    _stages.reconstruct(scheme, products, bias, output, rows, columns)
+    return output.reshape(*input_tensor.shape[:-1], columns)
+
+
+@torch.library.custom_op("rdna3_fastmm::linear", mutates_args=())
+def rdna3_linear(input_tensor: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    return _linear(Rank49Plan, "rdna3_fastmm::linear", input_tensor, weight, bias)
+
+
+@torch.library.custom_op("rdna3_fastmm::linear_rank7", mutates_args=())
+def rdna3_rank7_linear(
+    input_tensor: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None
+) -> torch.Tensor:
+    return _linear(Rank7Plan, "rdna3_fastmm::linear_rank7", input_tensor, weight, bias)
+
+
+@torch.library.custom_op("rdna3_fastmm::linear_rank48", mutates_args=())
+def rdna3_rank48_linear(
+    input_tensor: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None
+) -> torch.Tensor:
+    return _linear(Rank48Plan, "rdna3_fastmm::linear_rank48", input_tensor, weight, bias)
+
+
+def _fake_linear(input_tensor: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    return input_tensor.new_empty((*input_tensor.shape[:-1], weight.shape[0]))
+
+
+for _op in (rdna3_linear, rdna3_rank7_linear, rdna3_rank48_linear):
+    _op.register_fake(_fake_linear)
+
+RDNA3_LINEAR_OP = torch.ops.rdna3_fastmm.linear.default
+RDNA3_RANK7_LINEAR_OP = torch.ops.rdna3_fastmm.linear_rank7.default
+RDNA3_RANK48_LINEAR_OP = torch.ops.rdna3_fastmm.linear_rank48.default
+
+
+def _node_tensor(node: Node) -> Optional[torch.Tensor]:
+    value = node.meta.get("val", node.meta.get("example_value"))
+    return value if isinstance(value, torch.Tensor) else None
+
+
+def _has_linear_memory_budget(plan_type: type, shape: tuple, device: torch.device) -> bool:
+    """Temporaries of one dynamic call fit in half the free memory (linear.py:175-194)."""
+    rows, inner, columns = shape
+    s, rank = plan_type.scheme_size, plan_type.rank
+    mb, kb, nb = _ceil_div(rows, s), _ceil_div(inner, s), _ceil_div(columns, s)
+    allocation = rank * (mb * kb + kb * nb + mb * nb) * 2 + rows * columns * 2
+    free_bytes, _ = torch.cuda.mem_get_info(device)
+    return allocation <= free_bytes * MAX_LINEAR_ALLOCATION_FREE_FRACTION
+
+
+# Dispatch order of the rewrite: the first plan with a measured win is used.
+_REWRITE_ORDER: tuple = ((Rank7Plan, RDNA3_RANK7_LINEAR_OP), (Rank49Plan, RDNA3_LINEAR_OP))
+
+
+def _linear_node_target(node: Node) -> Optional[Callable]:
+    if node.op != "call_function" or node.target not in LINEAR_TARGETS:
+        return None
+    if node.kwargs or len(node.args) not in (2, 3):
+        return None
+    input_node, weight_node = node.args[:2]
+    bias_node = node.args[2] if len(node.args) == 3 else None
+    if not isinstance(input_node, Node) or not isinstance(weight_node, Node):
+        return None
+    input_tensor, weight = _node_tensor(input_node), _node_tensor(weight_node)
+    if input_tensor is None or weight is None or input_tensor.ndim < 2 or weight.ndim != 2:
+        return None
+    if input_tensor.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        return None
+    if input_tensor.device.type != "cuda" or weight.device != input_tensor.device:
+        return None
+    if not input_tensor.is_contiguous() or not weight.is_contiguous():
+        return None
+    inner = input_tensor.shape[-1]
+    columns, weight_inner = weight.shape
+    if inner != weight_inner:
+        return None
+    if not all(isinstance(d, int) for d in (*input_tensor.shape[:-1], inner, columns)):
+        return None
+    has_bias = bias_node is not None
+    if isinstance(bias_node, Node):
+        bias = _node_tensor(bias_node)
+        if (
+            bias is None
+            or tuple(bias.shape) != (columns,)
+            or bias.dtype != torch.bfloat16
+            or bias.device != input_tensor.device
+            or not bias.is_contiguous()
+        ):
+            return None
+    elif bias_node is not None:
+        return None
+    shape = (input_tensor.numel() // inner, inner, columns)
+    for plan_type, target in _REWRITE_ORDER:
+        plan: type[_LinearPlan] = plan_type
+        if plan.has_measured_linear_win(shape, has_bias=has_bias):
+            return target if _has_linear_memory_budget(plan, shape, input_tensor.device) else None
+    return None
+
+
+def rewrite_eligible_linears(graph_module: GraphModule, example_inputs: list) -> int:
+    """Replace eligible Linear nodes in place; returns how many were replaced."""
+    linear_nodes = tuple(
+        node for node in graph_module.graph.nodes if node.op == "call_function" and node.target in LINEAR_TARGETS
+    )
+    if any(
+        isinstance(argument, Node) and _node_tensor(argument) is None
+        for node in linear_nodes
+        for argument in node.args
+    ):
+        FakeTensorProp(graph_module).propagate(*example_inputs)
+    rewritten = 0
+    for node in linear_nodes:
+        target = _linear_node_target(node)
+        if target is None:
+            continue
+        input_node, weight_node = node.args[:2]
+        bias_node = node.args[2] if len(node.args) == 3 else None
+        with graph_module.graph.inserting_before(node):
+            replacement = graph_module.graph.call_function(target, args=(input_node, weight_node, bias_node))
+        replacement.meta = node.meta.copy()
+        node.replace_all_uses_with(replacement)
+        graph_module.graph.erase_node(node)
+        rewritten += 1
+    if rewritten:
+        graph_module.graph.lint()
+        graph_module.recompile()
+    return rewritten

@@ -1,0 +1,127 @@
+"""Every HIP stage against the CPU oracle on the same seeded inputs.
+
+Transforms and recombination are bit-exact (same fp32 program order, same
+round-to-nearest-even stores). Leaf products differ from the oracle's
+near-exact fp64 sum only by fp32 accumulation: the bound below is the
+standard ``K * 2^-24 * sum|a*b|`` (plus one fp16 ulp when stored as fp16).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fastmm_oracle as O
+from rdna3_fastmm import _stages
+from rdna3_fastmm.schemes import SCHEME_KEYS, load_scheme
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = (
+    (5, 6, 7),
+    (17, 19, 23),
+    (64, 64, 64),
+    (257, 263, 269),
+    (96, 128, 160),
+    (300, 256, 192),
+)
+DTYPES = (torch.bfloat16, torch.float16)
+DEVICE = torch.device("cuda", 0)
+
+
+def _ceil(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+def _inputs(shape, dtype, seed):
+    m, k, n = shape
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((m, k), generator=g).to(dtype)
+    w = (torch.randn((n, k), generator=g) / k**0.5).to(dtype)
+    bias = (torch.randn((n,), generator=g) * 0.02).to(dtype)
+    return x, w, bias
+
+
+def _np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy()
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().view(torch.int16).numpy()
+
+
+@pytest.mark.parametrize("key", SCHEME_KEYS)
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_transforms_bit_exact(key, shape, dtype) -> None:
+    print(f"\n[case] transforms {key} {shape} {dtype}", flush=True)
+    scheme = load_scheme(key)
+    oracle = O.load_oracle_scheme(key)
+    m, k, n = shape
+    s, r = scheme.size, scheme.rank
+    x, w, _ = _inputs(shape, dtype, seed=m + k + n)
+    xg, wg = x.to(DEVICE), w.to(DEVICE)
+    a = torch.empty((r, _ceil(m, s), _ceil(k, s)), device=DEVICE, dtype=torch.float16)
+    b = torch.empty((r, _ceil(n, s), _ceil(k, s)), device=DEVICE, dtype=torch.float16)
+    b2 = torch.empty_like(b)
+    _stages.left_transform(scheme, xg, a, m, k)
+    _stages.weight_transform(scheme, wg, b, n, k)
+    right = wg.t().contiguous()
+    _stages.right_transform(scheme, right, b2, k, n)
+    torch.cuda.synchronize()
+    expect_a = O.left_transform(oracle, _np(x)).view(np.int16)
+    expect_b = O.weight_transform(oracle, _np(w)).view(np.int16)
+    assert np.array_equal(_bits(a), expect_a)
+    assert np.array_equal(_bits(b), expect_b)
+    assert np.array_equal(_bits(b2), expect_b)
+
+
+@pytest.mark.parametrize("key", SCHEME_KEYS)
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("product_dtype", (torch.float16, torch.float32))
+def test_reconstruct_bit_exact(key, shape, product_dtype) -> None:
+    print(f"\n[case] reconstruct {key} {shape} {product_dtype}", flush=True)
+    scheme = load_scheme(key)
+    oracle = O.load_oracle_scheme(key)
+    m, _, n = shape
+    s, r = scheme.size, scheme.rank
+    g = torch.Generator().manual_seed(m * n)
+    products = torch.randn((r, _ceil(m, s), _ceil(n, s)), generator=g).to(product_dtype)
+    for dtype in DTYPES:
+        bias = (torch.randn((n,), generator=g) * 0.1).to(dtype)
+        for use_bias in (False, True):
+            out = torch.empty((m, n), device=DEVICE, dtype=dtype)
+            _stages.reconstruct(scheme, products.to(DEVICE), bias.to(DEVICE) if use_bias else None, out, m, n)
+            torch.cuda.synchronize()
+            expected = O.reconstruct(
+                oracle,
+                products.float().numpy() if product_dtype == torch.float32 else products.numpy(),
+                m,
+                n,
+                _np(bias) if use_bias else None,
+                "bf16" if dtype == torch.bfloat16 else "fp16",
+            )
+            assert np.array_equal(_bits(out), expected.view(np.int16)), (dtype, use_bias)
+
+
+@pytest.mark.parametrize(
+    "dims",
+    ((1, 5, 3, 7), (7, 33, 17, 129), (3, 256, 256, 64), (2, 300, 260, 136), (7, 129, 385, 2048), (5, 64, 64, 13)),
+)
+@pytest.mark.parametrize("product_dtype", (torch.float16, torch.float32))
+def test_leaf_products_within_fp32_accumulation_bound(dims, product_dtype) -> None:
+    rank, mb, nb, kb = dims
+    print(f"\n[case] leaf products {dims} {product_dtype}", flush=True)
+    g = torch.Generator().manual_seed(sum(dims))
+    a = torch.randn((rank, mb, kb), generator=g).half()
+    b = torch.randn((rank, nb, kb), generator=g).half()
+    p = torch.empty((rank, mb, nb), device=DEVICE, dtype=product_dtype)
+    _stages.leaf_products(rank, a.to(DEVICE), b.to(DEVICE), p, mb, kb, nb)
+    torch.cuda.synchronize()
+    exact = O.leaf_products(a.numpy(), b.numpy(), product_dtype="fp32")
+    magnitude = np.matmul(np.abs(a.numpy().astype(np.float64)), np.abs(np.swapaxes(b.numpy().astype(np.float64), 1, 2)))
+    bound = kb * 2.0**-24 * magnitude + 1e-30
+    got = p.float().cpu().numpy().astype(np.float64)
+    if product_dtype == torch.float16:
+        # one fp16 rounding of a value within `bound` of the exact sum
+        bound = bound + np.abs(exact.astype(np.float64)) * 2.0**-11 + 2.0**-24
+    assert np.all(np.abs(got - exact) <= bound)
