@@ -2,100 +2,314 @@
 //
 //   P[r] = A'[r] @ B'[r]^T,   A'[r]: [Mb, Kb], B'[r]: [Nb, Kb] (both K-contiguous)
 //
-// One workgroup (4 waves, 256 lanes) owns a BM x BN tile of one leaf. Each
-// wave owns a (BM/2) x (BN/2) sub-tile as a grid of 32x32 accumulators fed by
-// v_mfma_f32_32x32x16_f16 (fp32 accumulation). K advances in BK = 64 slices
-// staged through LDS, double-buffered: the global loads of slice k+1 are in
-// flight while the MFMAs of slice k run, and one barrier per slice separates
-// the LDS write of one buffer from the reads of the other.
+// Fast kernel (Kb % 32 == 0, Kb >= 96, 16-byte aligned operands): one
+// workgroup = 4 waves (one per SIMD) owns a 256 x 256 tile of one leaf; each
+// wave owns 128 x 128 as 4 x 4 v_mfma_f32_32x32x16_f16 accumulators (all 256
+// AGPRs). K advances in 32-wide slices through a 4-slot LDS ring filled by
+// direct-to-LDS loads (global_load_lds_dwordx4) three slices ahead, so a slice's
+// global latency is covered by three slices of MFMAs and no VGPRs stage data.
+// Per slice: the fragments of its second k-step are read while the first
+// k-step's MFMAs run; after a partial vmcnt wait (the next slice is resident)
+// and one barrier, the refill of the ring slot freed one slice earlier is
+// issued and the next slice's first fragments are read under the second
+// k-step's MFMAs. The refill is safe after that barrier because every wave
+// consumed (and waited for) its reads of the freed slot during the previous
+// slice.
 //
-// LDS layout: a slice is BM (or BN) rows of 64 halves = 8 chunks of 16 bytes.
-// Chunk c of row r lives at chunk position c ^ (r & 7), so the 16-byte reads
-// of 8 consecutive rows at one k (the MFMA operand pattern) and the 16-byte
-// writes of one row's 8 chunks both touch 8 distinct chunks = all 32 banks.
+// LDS layout: a slice row is 32 halves = 64 bytes = 4 chunks of 16 bytes;
+// chunk c of row r sits at c ^ ((r >> 2) & 3). gfx950's LDS is 64 banks wide,
+// so the 16 lanes of one ds_read_b128 phase (16 consecutive rows, one k) hit 16
+// distinct (row % 4, chunk) bank groups; the DMA writes 1 KB contiguous per
+// instruction (lane L -> slot L), so the swizzle is applied by choosing which
+// global chunk each lane fetches.
 //
-// MFMA operand convention: lane l supplies A[row l%32][k 8*(l/32) .. +7] and
-// B'[row l%32][same k]; because A and B use one lane->k map the contraction
-// is over all 16 k whatever order the hardware sums them in. The result
-// layout is the documented 32x32 one: lane l, element e holds
-// D[8*(e/4) + 4*(l/32) + e%4][l%32].
+// MFMA operands are passed as (B', A'): lane l supplies B'[n l%32][k 8*(l/32)
+// .. +7] and A'[m l%32][same k], so the accumulator holds P^T in the 32x32
+// layout and lane l, element e is P[m l%32][n 8*(e/4) + 4*(l/32) + e%4]: four
+// consecutive columns per lane. fp32 products leave as 16-byte stores; fp16
+// products are staged through LDS (row pitch 264 halves: 32 rows of 8-byte
+// writes spread over all 64 banks) and leave as coalesced 16-byte row
+// segments.
+//
+// Generic kernel (any Kb, any alignment): 256 x 256 tile, BK = 64, register-
+// staged loads with zero fill, double-buffered LDS; used for small or ragged
+// shapes where the fast kernel's preconditions fail.
 #include "abi_common.h"
 #include "fastmm_device.h"
 
 namespace fastmm {
 
 constexpr int kGemmThreads = 256;
-constexpr int kBK = 64;
+constexpr int kTile = 256;
 
-template <int BM, int BN>
-struct GemmShape {
-  static constexpr int WM = BM / 2;  // wave tile rows (2 x 2 waves)
-  static constexpr int WN = BN / 2;
-  static constexpr int TM = WM / 32;  // 32x32 accumulators per wave
-  static constexpr int TN = WN / 32;
-  static constexpr int A_CHUNKS = BM * kBK / 8 / kGemmThreads;  // 16-byte loads per lane
-  static constexpr int B_CHUNKS = BN * kBK / 8 / kGemmThreads;
-  static constexpr int STAGE_HALVES = (BM + BN) * kBK;
-  static constexpr int LDS_BYTES = 2 * STAGE_HALVES * 2;
-};
-
-__device__ __forceinline__ int swizzled(int row, int chunk) {
-  return row * kBK + ((chunk ^ (row & 7)) << 3);
-}
-
-// Map the linear workgroup id to (leaf, tile_m, tile_n). Workgroups are
-// dispatched round-robin over the 8 XCDs; renumber so each XCD works on a
-// contiguous range of tiles (they share A rows / B rows in that XCD's L2),
-// then walk tiles in column groups of `group` tile rows.
+// Workgroups are dispatched round-robin over the 8 XCDs; renumber so that each
+// XCD works on a contiguous range of tiles (tiles of one leaf share A'/B' rows
+// in that XCD's L2), then walk the tiles of a leaf in groups of `group` tile
+// rows, column by column.
 __device__ __forceinline__ void decode_tile(int wg, int total, int tiles_m, int tiles_n,
-                                            int& leaf, int& tm, int& tn) {
+                                            int group, int& leaf, int& tm, int& tn) {
   constexpr int kXcds = 8;
   int logical = wg;
-  if (total % kXcds == 0) {
-    const int per_xcd = total / kXcds;
-    logical = (wg % kXcds) * per_xcd + wg / kXcds;
-  }
+  if (total % kXcds == 0) logical = (wg % kXcds) * (total / kXcds) + wg / kXcds;
   const int per_leaf = tiles_m * tiles_n;
   leaf = logical / per_leaf;
-  int t = logical - leaf * per_leaf;
-  constexpr int group = 4;
-  const int group_span = group * tiles_n;
-  const int g = t / group_span;
+  const int t = logical - leaf * per_leaf;
+  const int g = t / (group * tiles_n);
   const int first_m = g * group;
   const int rows_in_group = min(group, tiles_m - first_m);
-  const int within = t - g * group_span;
+  const int within = t - g * group * tiles_n;
   tm = first_m + within % rows_in_group;
   tn = within / rows_in_group;
 }
 
-template <int BM, int BN, bool kAligned, int kOut>
+// ----------------------------------------------------------------- fast path
+
+namespace fast {
+
+constexpr int BK = 32;
+constexpr int STAGES = 4;
+constexpr int STAGE_HALVES = 2 * kTile * BK;
+constexpr int SEGMENTS = kTile / 16 / 4;  // 1 KB segments per operand per wave
+constexpr int OUT_PITCH = kTile + 8;       // halves per staged output row
+constexpr int LDS_BYTES = (STAGES * STAGE_HALVES * 2 > kTile * OUT_PITCH * 2)
+                              ? STAGES * STAGE_HALVES * 2
+                              : kTile * OUT_PITCH * 2;
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else if constexpr (N == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  else static_assert(N < 0, "unsupported vmcnt");
+}
+
+__device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+typedef const void __attribute__((address_space(1)))* global_ptr;
+typedef void __attribute__((address_space(3)))* lds_ptr;
+
+template <int kOut>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B,
                       void* __restrict__ P, int Mb, int Nb, int Kb, int tiles_m, int tiles_n,
                       int total_tiles) {
-  typedef GemmShape<BM, BN> G;
+  constexpr int TM = 4, TN = 4;  // 32x32 accumulators per wave (128 x 128)
   extern __shared__ __attribute__((aligned(16))) half_t smem[];
 
   int leaf, tm, tn;
-  decode_tile(blockIdx.x, total_tiles, tiles_m, tiles_n, leaf, tm, tn);
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
+  decode_tile(blockIdx.x, total_tiles, tiles_m, tiles_n, 8, leaf, tm, tn);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = tm * BM, n0 = tn * BN;
+  const int m0 = tm * kTile, n0 = tn * kTile;
   const half_t* a_leaf = A + static_cast<int64_t>(leaf) * Mb * Kb;
   const half_t* b_leaf = B + static_cast<int64_t>(leaf) * Nb * Kb;
 
-  uint4 a_regs[G::A_CHUNKS];
-  uint4 b_regs[G::B_CHUNKS];
-
-  auto load_rows = [&](const half_t* base, int row0, int rows, int k0, int chunks, uint4* regs) {
+  // DMA mapping: lane L of segment q writes row 16*q' + L/4, physical chunk L%4
+  // (q' = 4q + wave); it fetches the logical chunk stored there. Rows past the
+  // leaf are clamped onto its last row: they only feed outputs that are masked.
+  const int seg_row = lane >> 2;
+  int a_off[SEGMENTS], b_off[SEGMENTS];
 #pragma unroll
-    for (int i = 0; i < chunks; ++i) {
+  for (int q = 0; q < SEGMENTS; ++q) {
+    const int row = (q * 4 + wave) * 16 + seg_row;
+    const int chunk = (lane & 3) ^ ((row >> 2) & 3);
+    a_off[q] = min(m0 + row, Mb - 1) * Kb + chunk * 8;
+    b_off[q] = min(n0 + row, Nb - 1) * Kb + chunk * 8;
+  }
+  const int lane_row = lane & 31, lane_half = lane >> 5;
+  int rd_off[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    rd_off[ks] = lane_row * BK + (((2 * ks + lane_half) ^ ((lane_row >> 2) & 3)) << 3);
+  }
+  const int a_rd = wm * 128 * BK, b_rd = wn * 128 * BK;
+
+  half8 fa[2][TM], fb[2][TN];
+  float16v acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  auto load_slice = [&](int kt) {
+    half_t* as = smem + (kt % STAGES) * STAGE_HALVES;
+    half_t* bs = as + kTile * BK;
+    const int k0 = kt * BK;
+#pragma unroll
+    for (int q = 0; q < SEGMENTS; ++q) {
+      __builtin_amdgcn_global_load_lds((global_ptr)(a_leaf + a_off[q] + k0),
+                                       (lds_ptr)(as + (q * 4 + wave) * 16 * BK), 16, 0, 0);
+    }
+#pragma unroll
+    for (int q = 0; q < SEGMENTS; ++q) {
+      __builtin_amdgcn_global_load_lds((global_ptr)(b_leaf + b_off[q] + k0),
+                                       (lds_ptr)(bs + (q * 4 + wave) * 16 * BK), 16, 0, 0);
+    }
+  };
+  auto read_fragments = [&](int kt, int ks, int slot) {
+    const half_t* as = smem + (kt % STAGES) * STAGE_HALVES;
+    const half_t* bs = as + kTile * BK;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      fa[slot][i] = *reinterpret_cast<const half8*>(as + a_rd + i * 32 * BK + rd_off[ks]);
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      fb[slot][j] = *reinterpret_cast<const half8*>(bs + b_rd + j * 32 * BK + rd_off[ks]);
+    }
+  };
+  auto mfma = [&](int slot) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[slot][j], fa[slot][i], acc[i][j], 0, 0, 0);
+  };
+  // The 8 fragment reads go under the first 8 MFMAs (they are needed one
+  // k-step later); the refill loads, when present, under the second half.
+  auto schedule = [&](bool with_loads) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    if (with_loads) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      }
+    } else {
+      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    }
+  };
+
+  const int nk = Kb / BK;  // >= 3, checked by the launcher
+  load_slice(0);
+  load_slice(1);
+  load_slice(2);
+  wait_vmcnt<16>();
+  barrier();
+  read_fragments(0, 0, 0);
+
+  // kRefill: slice kt+3 exists; kNext: slice kt+1 exists; kWait: loads that may
+  // stay in flight while slice kt+1 must be resident (those of slice kt+2).
+  auto step = [&](int kt, auto refill_tag, auto next_tag, auto wait_tag) {
+    constexpr bool kRefill = decltype(refill_tag)::value;
+    constexpr bool kNext = decltype(next_tag)::value;
+    constexpr int kWait = decltype(wait_tag)::value;
+    read_fragments(kt, 1, 1);
+    mfma(0);
+    schedule(false);
+    if constexpr (kNext) wait_vmcnt<kWait>();
+    barrier();
+    if constexpr (kRefill) load_slice(kt + 3);
+    if constexpr (kNext) read_fragments(kt + 1, 0, 0);
+    mfma(1);
+    schedule(kRefill);
+  };
+  int kt = 0;
+  for (; kt < nk - 3; ++kt) {
+    step(kt, std::true_type{}, std::true_type{}, std::integral_constant<int, 8>{});
+  }
+  step(kt++, std::false_type{}, std::true_type{}, std::integral_constant<int, 8>{});
+  step(kt++, std::false_type{}, std::true_type{}, std::integral_constant<int, 0>{});
+  step(kt, std::false_type{}, std::false_type{}, std::integral_constant<int, 0>{});
+
+  const int64_t leaf_offset = static_cast<int64_t>(leaf) * Mb * Nb;
+  if constexpr (kOut == kFP32) {
+    // lane: row m0 + wm*128 + i*32 + lane_row, 4 columns per e-group.
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int row = m0 + wm * 128 + i * 32 + lane_row;
+      if (row >= Mb) continue;
+      float* out_row = static_cast<float*>(P) + leaf_offset + static_cast<int64_t>(row) * Nb;
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int col = n0 + wn * 128 + j * 32 + 8 * g + 4 * lane_half;
+          if (col < Nb) {
+            *reinterpret_cast<float4*>(out_row + col) =
+                make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                            acc[i][j][4 * g + 3]);
+          }
+        }
+    }
+  } else {
+    // Stage the 256 x 256 fp16 tile in LDS, then store 16-byte row segments.
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    uint16_t* staged = reinterpret_cast<uint16_t*>(smem);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int row = wm * 128 + i * 32 + lane_row;
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int col = wn * 128 + j * 32 + 8 * g + 4 * lane_half;
+          uint16_t h[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) h[e] = f32_to_fp16(acc[i][j][4 * g + e]);
+          store16<4>(staged + row * OUT_PITCH + col, h);
+        }
+    }
+    __syncthreads();
+    const int chunk = tid & 31;  // 32 chunks of 8 halves per row
+    uint16_t* out = static_cast<uint16_t*>(P) + leaf_offset;
+#pragma unroll 4
+    for (int pass = 0; pass < kTile / 8; ++pass) {
+      const int row = pass * 8 + (tid >> 5);
+      const int grow = m0 + row, gcol = n0 + chunk * 8;
+      if (grow < Mb && gcol < Nb) {
+        uint16_t h[8];
+        load16<8>(staged + row * OUT_PITCH + chunk * 8, h);
+        store16<8>(out + static_cast<int64_t>(grow) * Nb + gcol, h);
+      }
+    }
+  }
+}
+
+}  // namespace fast
+
+// -------------------------------------------------------------- generic path
+
+namespace generic {
+
+constexpr int BK = 64;
+constexpr int A_CHUNKS = kTile * BK / 8 / kGemmThreads;
+constexpr int STAGE_HALVES = 2 * kTile * BK;
+constexpr int LDS_BYTES = 2 * STAGE_HALVES * 2;
+
+// Chunk c (8 halves) of row r at c ^ (r & 7).
+__device__ __forceinline__ int swizzled(int row, int chunk) {
+  return row * BK + ((chunk ^ (row & 7)) << 3);
+}
+
+template <bool kAligned, int kOut>
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B,
+                      void* __restrict__ P, int Mb, int Nb, int Kb, int tiles_m, int tiles_n,
+                      int total_tiles) {
+  constexpr int TM = 4, TN = 4;
+  extern __shared__ __attribute__((aligned(16))) half_t smem[];
+  int leaf, tm, tn;
+  decode_tile(blockIdx.x, total_tiles, tiles_m, tiles_n, 4, leaf, tm, tn);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int m0 = tm * kTile, n0 = tn * kTile;
+  const half_t* a_leaf = A + static_cast<int64_t>(leaf) * Mb * Kb;
+  const half_t* b_leaf = B + static_cast<int64_t>(leaf) * Nb * Kb;
+
+  uint4 a_regs[A_CHUNKS], b_regs[A_CHUNKS];
+  auto load_rows = [&](const half_t* base, int row0, int rows, int k0, uint4* regs) {
+#pragma unroll
+    for (int i = 0; i < A_CHUNKS; ++i) {
       const int id = i * kGemmThreads + tid;
-      const int row = id >> 3;
+      const int grow = row0 + (id >> 3);
       const int k = k0 + ((id & 7) << 3);
-      const int grow = row0 + row;
       uint4 v = make_uint4(0, 0, 0, 0);
       if (grow < rows) {
         const half_t* p = base + static_cast<int64_t>(grow) * Kb + k;
@@ -104,127 +318,117 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
         } else {
           uint16_t h[8];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            h[e] = (k + e < Kb) ? __builtin_bit_cast(uint16_t, p[e]) : uint16_t{0};
-          }
+          for (int e = 0; e < 8; ++e) h[e] = (k + e < Kb) ? __builtin_bit_cast(uint16_t, p[e]) : uint16_t{0};
           __builtin_memcpy(&v, h, 16);
         }
       }
       regs[i] = v;
     }
   };
-  auto global_load = [&](int k0) {
-    load_rows(a_leaf, m0, Mb, k0, G::A_CHUNKS, a_regs);
-    load_rows(b_leaf, n0, Nb, k0, G::B_CHUNKS, b_regs);
-  };
   auto lds_store = [&](int buffer) {
-    half_t* as = smem + buffer * G::STAGE_HALVES;
-    half_t* bs = as + BM * kBK;
+    half_t* as = smem + buffer * STAGE_HALVES;
+    half_t* bs = as + kTile * BK;
 #pragma unroll
-    for (int i = 0; i < G::A_CHUNKS; ++i) {
+    for (int i = 0; i < A_CHUNKS; ++i) {
       const int id = i * kGemmThreads + tid;
       *reinterpret_cast<uint4*>(as + swizzled(id >> 3, id & 7)) = a_regs[i];
-    }
-#pragma unroll
-    for (int i = 0; i < G::B_CHUNKS; ++i) {
-      const int id = i * kGemmThreads + tid;
       *reinterpret_cast<uint4*>(bs + swizzled(id >> 3, id & 7)) = b_regs[i];
     }
   };
 
-  float16v acc[G::TM][G::TN];
+  float16v acc[TM][TN];
 #pragma unroll
-  for (int i = 0; i < G::TM; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < G::TN; ++j)
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  const int k_tiles = (Kb + kBK - 1) / kBK;
-  global_load(0);
+  const int k_tiles = (Kb + BK - 1) / BK;
+  load_rows(a_leaf, m0, Mb, 0, a_regs);
+  load_rows(b_leaf, n0, Nb, 0, b_regs);
   lds_store(0);
   __syncthreads();
-
-  const int lane_row = lane & 31;
-  const int lane_chunk = lane >> 5;
+  const int lane_row = lane & 31, lane_half = lane >> 5;
   for (int kt = 0; kt < k_tiles; ++kt) {
     const int buffer = kt & 1;
-    if (kt + 1 < k_tiles) global_load((kt + 1) * kBK);
-    const half_t* as = smem + buffer * G::STAGE_HALVES;
-    const half_t* bs = as + BM * kBK;
+    if (kt + 1 < k_tiles) {
+      load_rows(a_leaf, m0, Mb, (kt + 1) * BK, a_regs);
+      load_rows(b_leaf, n0, Nb, (kt + 1) * BK, b_regs);
+    }
+    const half_t* as = smem + buffer * STAGE_HALVES;
+    const half_t* bs = as + kTile * BK;
 #pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      const int chunk = 2 * ks + lane_chunk;
-      half8 af[G::TM], bf[G::TN];
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      const int chunk = 2 * ks + lane_half;
+      half8 af[TM], bf[TN];
 #pragma unroll
-      for (int i = 0; i < G::TM; ++i) {
-        const int row = wm * G::WM + i * 32 + lane_row;
-        af[i] = *reinterpret_cast<const half8*>(as + swizzled(row, chunk));
-      }
+      for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const half8*>(as + swizzled(wm * 128 + i * 32 + lane_row, chunk));
 #pragma unroll
-      for (int j = 0; j < G::TN; ++j) {
-        const int row = wn * G::WN + j * 32 + lane_row;
-        bf[j] = *reinterpret_cast<const half8*>(bs + swizzled(row, chunk));
-      }
+      for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const half8*>(bs + swizzled(wn * 128 + j * 32 + lane_row, chunk));
 #pragma unroll
-      for (int i = 0; i < G::TM; ++i)
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < G::TN; ++j)
+        for (int j = 0; j < TN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
     }
     if (kt + 1 < k_tiles) lds_store(buffer ^ 1);
     __syncthreads();
   }
 
-  // Epilogue: lane l, element e of accumulator (i, j) is
-  // row 8*(e/4) + 4*(l/32) + e%4, column l%32 of that 32x32 block.
+  // lane l, element e of accumulator (i, j): row 8*(e/4) + 4*(l/32) + e%4,
+  // column l%32 of that 32x32 block.
   const int64_t leaf_offset = static_cast<int64_t>(leaf) * Mb * Nb;
 #pragma unroll
-  for (int i = 0; i < G::TM; ++i) {
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < G::TN; ++j) {
-      const int col = n0 + wn * G::WN + j * 32 + lane_row;
+    for (int j = 0; j < TN; ++j) {
+      const int col = n0 + wn * 128 + j * 32 + lane_row;
       if (col >= Nb) continue;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int row = m0 + wm * G::WM + i * 32 + 8 * (e >> 2) + 4 * lane_chunk + (e & 3);
+        const int row = m0 + wm * 128 + i * 32 + 8 * (e >> 2) + 4 * lane_half + (e & 3);
         if (row < Mb) {
           const int64_t offset = leaf_offset + static_cast<int64_t>(row) * Nb + col;
-          if constexpr (kOut == kFP32) {
-            static_cast<float*>(P)[offset] = acc[i][j][e];
-          } else {
-            static_cast<uint16_t*>(P)[offset] = f32_to_fp16(acc[i][j][e]);
-          }
+          if constexpr (kOut == kFP32) static_cast<float*>(P)[offset] = acc[i][j][e];
+          else static_cast<uint16_t*>(P)[offset] = f32_to_fp16(acc[i][j][e]);
         }
       }
     }
-  }
 }
 
-template <int BM, int BN, bool kAligned, int kOut>
-int launch_leaf_gemm(const void* a, const void* b, void* p, int64_t rank, int64_t mb, int64_t kb,
-                     int64_t nb, hipStream_t stream) {
-  typedef GemmShape<BM, BN> G;
-  auto kernel = leaf_gemm_kernel<BM, BN, kAligned, kOut>;
-  static bool configured = false;
+}  // namespace generic
+
+// ---------------------------------------------------------------- launchers
+
+template <class Kernel>
+int launch_tiles(Kernel kernel, int lds_bytes, const void* a, const void* b, void* p,
+                 int64_t rank, int64_t mb, int64_t kb, int64_t nb, hipStream_t stream) {
+  static bool configured = false;  // one per kernel instantiation
   if (!configured) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                            G::LDS_BYTES) != hipSuccess) {
-      return fail(FASTMM_ERROR_LAUNCH, "leaf products: cannot reserve %d bytes of LDS",
-                  G::LDS_BYTES);
+                            hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes) != hipSuccess) {
+      return fail(FASTMM_ERROR_LAUNCH, "leaf products: cannot reserve %d bytes of LDS", lds_bytes);
     }
     configured = true;
   }
-  const int64_t tiles_m = ceil_div(mb, BM);
-  const int64_t tiles_n = ceil_div(nb, BN);
+  const int64_t tiles_m = ceil_div(mb, kTile);
+  const int64_t tiles_n = ceil_div(nb, kTile);
   const int64_t total = tiles_m * tiles_n * rank;
   if (total > INT32_MAX) return fail(FASTMM_ERROR_UNSUPPORTED, "leaf products: too many tiles");
-  kernel<<<dim3(static_cast<unsigned>(total)), kGemmThreads, G::LDS_BYTES, stream>>>(
+  kernel<<<dim3(static_cast<unsigned>(total)), kGemmThreads, lds_bytes, stream>>>(
       static_cast<const half_t*>(a), static_cast<const half_t*>(b), p, static_cast<int>(mb),
       static_cast<int>(nb), static_cast<int>(kb), static_cast<int>(tiles_m),
       static_cast<int>(tiles_n), static_cast<int>(total));
   return check_launch("leaf products");
+}
+
+// The fast kernel's preconditions; the generic kernel handles everything else.
+bool fast_leaf_gemm_applies(const void* a, const void* b, const void* p, int64_t kb, int64_t nb,
+                            int products_dtype) {
+  const int64_t out_align = products_dtype == kFP32 ? 4 : 8;
+  return kb % fast::BK == 0 && kb >= 3 * fast::BK && nb % out_align == 0 && aligned_to(a, 16) &&
+         aligned_to(b, 16) && aligned_to(p, 16);
 }
 
 }  // namespace fastmm
@@ -250,24 +454,25 @@ extern "C" int fastmm_leaf_products(int rank, const void* left_transformed,
     return fail(FASTMM_ERROR_UNSUPPORTED, "leaf products: plane larger than 2^31 elements");
   }
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool aligned = block_inner % 8 == 0 && aligned_to(left_transformed, 16) &&
-                       aligned_to(right_transformed, 16);
+  const void* a = left_transformed;
+  const void* b = right_transformed;
+  void* p = products;
+  const int64_t mb = block_rows, kb = block_inner, nb = block_columns;
+  if (fast_leaf_gemm_applies(a, b, p, kb, nb, products_dtype)) {
+    if (products_dtype == kFP32) {
+      return launch_tiles(fast::leaf_gemm_kernel<kFP32>, fast::LDS_BYTES, a, b, p, rank, mb, kb, nb, s);
+    }
+    return launch_tiles(fast::leaf_gemm_kernel<kFP16>, fast::LDS_BYTES, a, b, p, rank, mb, kb, nb, s);
+  }
+  const bool aligned = kb % 8 == 0 && aligned_to(a, 16) && aligned_to(b, 16);
   if (aligned) {
     if (products_dtype == kFP32) {
-      return launch_leaf_gemm<256, 256, true, kFP32>(left_transformed, right_transformed, products,
-                                                     rank, block_rows, block_inner,
-                                                     block_columns, s);
+      return launch_tiles(generic::leaf_gemm_kernel<true, kFP32>, generic::LDS_BYTES, a, b, p, rank, mb, kb, nb, s);
     }
-    return launch_leaf_gemm<256, 256, true, kFP16>(left_transformed, right_transformed, products,
-                                                   rank, block_rows, block_inner, block_columns,
-                                                   s);
+    return launch_tiles(generic::leaf_gemm_kernel<true, kFP16>, generic::LDS_BYTES, a, b, p, rank, mb, kb, nb, s);
   }
   if (products_dtype == kFP32) {
-    return launch_leaf_gemm<256, 256, false, kFP32>(left_transformed, right_transformed, products,
-                                                    rank, block_rows, block_inner, block_columns,
-                                                    s);
+    return launch_tiles(generic::leaf_gemm_kernel<false, kFP32>, generic::LDS_BYTES, a, b, p, rank, mb, kb, nb, s);
   }
-  return launch_leaf_gemm<256, 256, false, kFP16>(left_transformed, right_transformed, products,
-                                                  rank, block_rows, block_inner, block_columns,
-                                                  s);
+  return launch_tiles(generic::leaf_gemm_kernel<false, kFP16>, generic::LDS_BYTES, a, b, p, rank, mb, kb, nb, s);
 }

@@ -105,7 +105,12 @@ def test_reconstruct_bit_exact(key, shape, product_dtype) -> None:
 
 @pytest.mark.parametrize(
     "dims",
-    ((1, 5, 3, 7), (7, 33, 17, 129), (3, 256, 256, 64), (2, 300, 260, 136), (7, 129, 385, 2048), (5, 64, 64, 13)),
+    (
+        # generic kernel: ragged or short K, unaligned rows
+        (1, 5, 3, 7), (7, 33, 17, 129), (3, 256, 256, 64), (2, 300, 260, 136), (7, 129, 385, 2048), (5, 64, 64, 13),
+        # fast kernel: Kb % 32 == 0 and Kb >= 96, ragged Mb / Nb tails, one and many K slices
+        (2, 300, 264, 96), (3, 513, 520, 128), (7, 256, 256, 2048), (1, 4107, 16, 192), (2, 40, 8, 3072),
+    ),
 )
 @pytest.mark.parametrize("product_dtype", (torch.float16, torch.float32))
 def test_leaf_products_within_fp32_accumulation_bound(dims, product_dtype) -> None:
