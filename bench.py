@@ -87,6 +87,21 @@ def _median(values: list[float]) -> float:
     return ordered[len(ordered) // 2]
 
 
+def measured_traffic(config: str) -> float | None:
+    """HBM-side bytes per leaf-GEMM launch from the committed rocprofv3 summary, if any.
+
+    profiles/leaf_gemm_traffic_<config>.md holds FETCH_SIZE + WRITE_SIZE of the
+    same workload, scaled by a 1 GiB copy (see that file for the commands).
+    """
+    path = REPO_ROOT / "profiles" / f"leaf_gemm_traffic_{config}.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch"):
+            return float(line.split(":")[1])
+    return None
+
+
 def cpu_baseline(cfg: dict, x, w, b, budget_s: float) -> dict:
     """Time the CPU oracle on a row sample of the workload; TFLOP/s of that sample."""
     import numpy as np
@@ -142,6 +157,11 @@ def main() -> int:
     parser.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     parser.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     parser.add_argument("--no-cpu", action="store_true")
+    parser.add_argument(
+        "--traffic-calibration",
+        action="store_true",
+        help="also run three 1 GiB device copies (a kernel of known HBM traffic) for counter scaling",
+    )
     args = parser.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: every box in this setup has one MI355X, and the "
@@ -171,9 +191,10 @@ def main() -> int:
             plan.run_linear_packed(x, packed, workspace, b, out)
 
         def native():
-            torch.mm(x, w.T, out=native_out)
-            if b is not None:
-                native_out.add_(b)
+            if b is None:
+                torch.mm(x, w.T, out=native_out)
+            else:
+                torch.addmm(b, x, w.T, out=native_out)
     else:
         def step():
             plan.run_linear(x, w, workspace, b)
@@ -181,6 +202,13 @@ def main() -> int:
         def native():
             torch.nn.functional.linear(x, w, b)
 
+    if args.traffic_calibration:
+        source = torch.empty(1 << 29, device=device, dtype=torch.float16)
+        target = torch.empty_like(source)
+        for _ in range(3):
+            target.copy_(source)
+        torch.cuda.synchronize()
+        del source, target
     for _ in range(args.warmup):
         step()
         native()
@@ -248,7 +276,9 @@ def main() -> int:
         "native_bf16": {
             "ms_per_step": round(native_ms, 4),
             "tflops": round(flops / (native_ms * 1e-3) / 1e12, 2),
-            "op": "torch.mm(out=)+bias" if cfg["prepacked"] else "torch.nn.functional.linear",
+            "op": ("torch.addmm(bias, x, W.T, out=)" if b is not None else "torch.mm(x, W.T, out=)")
+            if cfg["prepacked"]
+            else "torch.nn.functional.linear",
             "blas": str(torch.backends.cuda.preferred_blas_library()),
             "TORCH_BLAS_PREFER_HIPBLASLT": os.environ.get("TORCH_BLAS_PREFER_HIPBLASLT"),
         },
@@ -269,7 +299,7 @@ def main() -> int:
             "peak": MFMA_FP16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(leaf_tflops / MFMA_FP16_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(args.config),
             "work_per_launch": f"2*R*Mb*Kb*Nb = {leaf_flops:.4e} flop",
         },
     }

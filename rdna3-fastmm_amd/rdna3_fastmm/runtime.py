@@ -173,6 +173,17 @@ def is_tested_runtime(device: torch.device) -> bool:
     return unsupported_runtime_reason(device) is None
 
 
+# ------------------------------------------------------------- dispatch data
+
+# Shape families where a plan beat native BF16 torch.mm / F.linear on one
+# MI355X, with the measurement that showed it. The rewrite and
+# is_linear_recommended only ever select a family listed here. Measured so far
+# (bench.py, kernel-trace medians): rank-7 C3 0.87x, rank-48 8192^3 0.62x,
+# rank-49 C4 0.72x, rank-7 C2 0.51x of native -- no win yet, so the tables
+# below are empty and the graph rewrite leaves every Linear on native BF16.
+MEASURED_WINS: dict[LinearShapeFamily, str] = {}
+
+
 # ---------------------------------------------------------------------- plans
 
 _VERIFIED_SCHEMES: set[int] = set()

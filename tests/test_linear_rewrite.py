@@ -1,0 +1,164 @@
+"""The FX Linear rewrite and the Dynamo backend, on the CPU with fake CUDA tensors.
+
+Mirrors reference tests/test_inductor.py:34-203: eligible BF16 Linears are
+replaced by the rdna3_fastmm operators only for measured-win families and
+within the memory budget; everything else is left alone; the backend hands
+the graph to Inductor with CUDA graphs off only when it rewrote something.
+"""
+
+import pytest
+import torch
+from torch._subclasses.fake_tensor import FakeTensorMode
+
+from rdna3_fastmm import inductor, linear
+from rdna3_fastmm.linear import (
+    RDNA3_LINEAR_OP,
+    RDNA3_RANK7_LINEAR_OP,
+    _linear_node_target,
+    rewrite_eligible_linears,
+)
+from rdna3_fastmm.runtime import LinearShapeFamily, Rank7Plan, Rank49Plan
+
+
+class Linear(torch.nn.Module):
+    def forward(self, input_tensor, weight):
+        return torch.nn.functional.linear(input_tensor, weight)
+
+
+class BiasLinear(torch.nn.Module):
+    def forward(self, input_tensor, weight, bias):
+        return torch.nn.functional.linear(input_tensor, weight, bias)
+
+
+def fake(*shapes, dtype=torch.bfloat16, device="cuda"):
+    mode = FakeTensorMode(allow_non_fake_inputs=True)
+    with mode:
+        return [torch.empty(shape, dtype=dtype, device=device) for shape in shapes], mode
+
+
+def traced(module, *tensors):
+    graph_module = torch.fx.symbolic_trace(module)
+    placeholders = [n for n in graph_module.graph.nodes if n.op == "placeholder"]
+    for node, tensor in zip(placeholders, tensors):
+        node.meta["val"] = tensor
+    return graph_module
+
+
+def targets(graph_module):
+    return {node.target for node in graph_module.graph.nodes if node.op == "call_function"}
+
+
+@pytest.fixture
+def measured(monkeypatch):
+    monkeypatch.setattr(Rank7Plan, "linear_shape_families", (LinearShapeFamily(3_328, 9_216, 4_608, 12_288, False),))
+    monkeypatch.setattr(Rank49Plan, "linear_shape_families", (LinearShapeFamily(19_968, 19_968, 4_096, 16_384, True),))
+    monkeypatch.setattr(torch.cuda, "mem_get_info", lambda device=None: (200 << 30, 288 << 30))
+
+
+def test_rewrite_replaces_eligible_bfloat16_linear(measured) -> None:
+    (x, w), _ = fake((5120, 4608), (12288, 4608))
+    gm = traced(Linear(), x, w)
+    assert rewrite_eligible_linears(gm, [x, w]) == 1
+    assert RDNA3_RANK7_LINEAR_OP in targets(gm)
+
+
+def test_rewrite_keeps_rank49_for_exact_family(measured) -> None:
+    (x, w, b), _ = fake((19_968, 4_096), (16_384, 4_096), (16_384,))
+    gm = traced(BiasLinear(), x, w, b)
+    assert rewrite_eligible_linears(gm, [x, w, b]) == 1
+    assert RDNA3_LINEAR_OP in targets(gm)
+
+
+def test_rewrite_flattens_leading_dimensions(measured) -> None:
+    (x, w), _ = fake((2, 2560, 4608), (12288, 4608))
+    gm = traced(Linear(), x, w)
+    assert rewrite_eligible_linears(gm, [x, w]) == 1
+
+
+@pytest.mark.parametrize(
+    "shapes, dtype, device",
+    (
+        (((3072, 4608), (12288, 4608)), torch.bfloat16, "cuda"),  # rows outside the family
+        (((5120, 4608), (12288, 4608)), torch.float16, "cuda"),  # not BF16
+        (((5120, 4608), (12288, 4608)), torch.bfloat16, "cpu"),  # not on the GPU
+    ),
+)
+def test_rewrite_preserves_ineligible_linear(measured, shapes, dtype, device) -> None:
+    (x, w), _ = fake(*shapes, dtype=dtype, device=device)
+    gm = traced(Linear(), x, w)
+    assert rewrite_eligible_linears(gm, [x, w]) == 0
+
+
+def test_rewrite_preserves_linear_without_memory_budget(measured, monkeypatch) -> None:
+    monkeypatch.setattr(torch.cuda, "mem_get_info", lambda device=None: (1 << 20, 288 << 30))
+    (x, w), _ = fake((5120, 4608), (12288, 4608))
+    gm = traced(Linear(), x, w)
+    assert rewrite_eligible_linears(gm, [x, w]) == 0
+
+
+def test_rewrite_rejects_non_contiguous_weight(measured) -> None:
+    (x, w), mode = fake((5120, 4608), (4608, 12288))
+    with mode:
+        wt = w.t()
+    gm = traced(Linear(), x, wt)
+    assert _linear_node_target(next(n for n in gm.graph.nodes if n.op == "call_function")) is None
+
+
+def test_shipped_tables_leave_graphs_untouched(monkeypatch) -> None:
+    """With no measured MI355X win the rewrite must not fire."""
+    monkeypatch.setattr(torch.cuda, "mem_get_info", lambda device=None: (200 << 30, 288 << 30))
+    (x, w), _ = fake((5120, 4608), (12288, 4608))
+    gm = traced(Linear(), x, w)
+    assert rewrite_eligible_linears(gm, [x, w]) == 0
+
+
+def test_operators_are_registered_with_fake_kernels() -> None:
+    for name in ("linear", "linear_rank7", "linear_rank48"):
+        assert hasattr(torch.ops.rdna3_fastmm, name)
+    (x, w, b), mode = fake((2, 3, 19), (23, 19), (23,))
+    with mode:
+        out = torch.ops.rdna3_fastmm.linear_rank7(x, w, b)
+    assert tuple(out.shape) == (2, 3, 23) and out.dtype == torch.bfloat16
+
+
+def test_backend_disables_cudagraphs_only_after_a_rewrite(monkeypatch) -> None:
+    captured = {}
+
+    def fake_compile(graph, example_inputs, options):
+        captured["options"] = options
+        return object()
+
+    gm = torch.fx.symbolic_trace(lambda value: value.sin())
+    monkeypatch.setattr(torch._inductor, "compile", fake_compile)
+    monkeypatch.setattr(inductor, "_enable_rewrite", lambda: True)
+    monkeypatch.setattr(inductor, "rewrite_eligible_linears", lambda graph, inputs: 1)
+    inductor.compile_backend(gm, [torch.randn(4)], mode="reduce-overhead")
+    assert captured["options"]["triton.cudagraphs"] is False
+
+    monkeypatch.setattr(inductor, "rewrite_eligible_linears", lambda graph, inputs: 0)
+    inductor.compile_backend(gm, [torch.randn(4)], mode="reduce-overhead")
+    assert captured["options"] == {"triton.cudagraphs": True}
+
+
+def test_backend_preserves_standard_inductor_when_runtime_is_unsupported(monkeypatch) -> None:
+    captured = {}
+    monkeypatch.setattr(torch._inductor, "compile", lambda g, i, options: captured.update(options=options))
+    monkeypatch.setattr(inductor, "_enable_rewrite", lambda: False)
+    inductor.compile_backend(torch.fx.symbolic_trace(lambda v: v.cos()), [torch.randn(4)], mode="reduce-overhead")
+    assert captured["options"] == {"triton.cudagraphs": True}
+
+
+def test_pyproject_registers_named_dynamo_backend() -> None:
+    from pathlib import Path
+
+    import tomli
+
+    pyproject = tomli.loads((Path(__file__).resolve().parent.parent / "pyproject.toml").read_text())
+    assert pyproject["project"]["entry-points"]["torch_dynamo_backends"] == {
+        "rdna3-fastmm": "rdna3_fastmm.inductor:compile_backend"
+    }
+
+
+def test_linear_ops_reject_bad_operands() -> None:
+    with pytest.raises(ValueError, match="bf16 or fp16"):
+        linear._check_operands("op", torch.empty(2, 3), torch.empty(4, 3), None)

@@ -1,0 +1,76 @@
+"""The C ABI library: loads without a GPU, exports every declared symbol, reports
+argument errors before any launch, and carries the verified certificates' digests."""
+
+import ctypes
+from pathlib import Path
+import re
+
+import pytest
+
+from rdna3_fastmm import _native
+from rdna3_fastmm.schemes import SCHEME_KEYS, load_scheme
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "fastmm_amd.h"
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(fastmm_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_stage_entry_points() -> None:
+    names = declared_functions()
+    for required in (
+        "fastmm_left_transform",
+        "fastmm_weight_transform",
+        "fastmm_right_transform",
+        "fastmm_leaf_products",
+        "fastmm_reconstruct",
+        "fastmm_abi_version",
+        "fastmm_last_error",
+    ):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol() -> None:
+    lib = _native.library()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.fastmm_abi_version() == _native.ABI_VERSION
+
+
+def test_compiled_scheme_digests_match_verified_certificates() -> None:
+    lib = _native.library()
+    for key in SCHEME_KEYS:
+        scheme = load_scheme(key)
+        size, rank = ctypes.c_int(), ctypes.c_int()
+        assert lib.fastmm_scheme_info(scheme.scheme_id, ctypes.byref(size), ctypes.byref(rank)) == 0
+        assert (size.value, rank.value) == (scheme.size, scheme.rank)
+        assert _native.scheme_sha256(scheme.scheme_id) == scheme.certificate_sha256
+    assert lib.fastmm_scheme_info(7, None, None) == 1
+    assert b"unknown scheme" in lib.fastmm_last_error()
+
+
+@pytest.mark.parametrize(
+    ("call", "message"),
+    (
+        (lambda lib: lib.fastmm_left_transform(0, 0, None, None, 4, 4, None), b"null pointer"),
+        (lambda lib: lib.fastmm_left_transform(0, 2, 16, 16, 4, 4, None), b"dtype"),
+        (lambda lib: lib.fastmm_weight_transform(0, 0, 16, 16, 0, 4, None), b"positive"),
+        (lambda lib: lib.fastmm_right_transform(1, 1, 16, 16, 4, -1, None), b"positive"),
+        (lambda lib: lib.fastmm_leaf_products(7, 16, 16, 16, 0, 2, 2, 2, None), b"fp16 or fp32"),
+        (lambda lib: lib.fastmm_leaf_products(0, 16, 16, 16, 1, 2, 2, 2, None), b"positive"),
+        (lambda lib: lib.fastmm_leaf_products(7, 16, 16, 16, 1, 1 << 20, 1 << 12, 2, None), b"2^31"),
+        (lambda lib: lib.fastmm_reconstruct(0, 0, 16, None, 0, 16, 4, 4, None), b"fp16 or fp32"),
+        (lambda lib: lib.fastmm_reconstruct(9, 1, 16, None, 0, 16, 4, 4, None), b"unknown scheme"),
+    ),
+)
+def test_argument_errors_are_reported_before_any_launch(call, message) -> None:
+    lib = _native.library()
+    assert call(lib) != 0
+    assert message in lib.fastmm_last_error()
+
+
+def test_missing_library_fails_loudly(tmp_path: Path) -> None:
+    with pytest.raises(_native.NativeLibraryError, match="not built"):
+        _native.library(str(tmp_path / "libfastmm_amd.so"))

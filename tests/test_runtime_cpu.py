@@ -1,0 +1,157 @@
+"""Plan logic that needs no GPU: shape partition, byte formulas, gates, validation.
+
+Mirrors the reference's CPU-safe tests (tests/test_rdna3.py:32-403), with the
+runtime gate retargeted to one MI355X and the device faked by monkeypatch.
+"""
+
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+from rdna3_fastmm import runtime
+from rdna3_fastmm.runtime import (
+    LinearShapeFamily,
+    MatrixShape,
+    Rank7Plan,
+    Rank48Plan,
+    Rank49Plan,
+    unsupported_runtime_reason,
+)
+
+
+def configure_supported_runtime(monkeypatch: pytest.MonkeyPatch) -> None:
+    monkeypatch.setattr(torch.version, "hip", "7.0.51831")
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
+    monkeypatch.setattr(torch.cuda, "current_device", lambda: 0)
+    monkeypatch.setattr(
+        torch.cuda,
+        "get_device_properties",
+        lambda device: SimpleNamespace(gcnArchName="gfx950:sramecc+:xnack-", multi_processor_count=256),
+    )
+    monkeypatch.setattr(torch, "__version__", "2.10.0+rocm7.0")
+
+
+def test_runtime_accepts_tested_stack(monkeypatch) -> None:
+    configure_supported_runtime(monkeypatch)
+    assert unsupported_runtime_reason() is None
+
+
+def test_runtime_requires_rocm_build(monkeypatch) -> None:
+    monkeypatch.setattr(torch.version, "hip", None)
+    assert unsupported_runtime_reason() == "requires a ROCm PyTorch build"
+
+
+def test_runtime_requires_available_gpu(monkeypatch) -> None:
+    configure_supported_runtime(monkeypatch)
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: False)
+    assert unsupported_runtime_reason() == "requires an available ROCm GPU"
+
+
+def test_runtime_rejects_cpu_device(monkeypatch) -> None:
+    configure_supported_runtime(monkeypatch)
+    assert unsupported_runtime_reason(torch.device("cpu")) == "requires a ROCm GPU device"
+
+
+def test_runtime_describes_wrong_gpu(monkeypatch) -> None:
+    configure_supported_runtime(monkeypatch)
+    monkeypatch.setattr(
+        torch.cuda, "get_device_properties", lambda d: SimpleNamespace(gcnArchName="gfx942", multi_processor_count=304)
+    )
+    assert unsupported_runtime_reason() == "tested only on gfx950 with 256 compute units; found gfx942 with 304"
+
+
+@pytest.mark.parametrize(
+    ("component", "version", "expected"),
+    (
+        ("torch", "2.9.1+rocm6.4", "tested only with PyTorch 2.10.0; found 2.9.1+rocm6.4"),
+        ("hip", "6.4.1", "tested only with ROCm 7.0; found 6.4.1"),
+    ),
+)
+def test_runtime_describes_version_mismatch(monkeypatch, component, version, expected) -> None:
+    configure_supported_runtime(monkeypatch)
+    if component == "torch":
+        monkeypatch.setattr(torch, "__version__", version)
+    else:
+        monkeypatch.setattr(torch.version, "hip", version)
+    assert unsupported_runtime_reason() == expected
+
+
+def test_shape_uses_padded_quarters() -> None:
+    shape = MatrixShape.from_dimensions(257, 263, 269, 4)
+    assert shape.dimensions == (257, 263, 269)
+    assert (shape.block_rows, shape.block_inner, shape.block_columns) == (65, 66, 68)
+    assert shape.workspace_elements(49) == 49 * (65 * 66 + 66 * 68 + 65 * 68)
+
+
+def test_shape_rejects_nonpositive_dimensions() -> None:
+    with pytest.raises(ValueError, match="positive"):
+        MatrixShape.from_dimensions(4, 0, 4, 4)
+
+
+@pytest.mark.parametrize("plan_type", (Rank7Plan, Rank48Plan, Rank49Plan))
+def test_plans_reject_cpu_device(plan_type) -> None:
+    with pytest.raises(ValueError, match="ROCm"):
+        plan_type(4, 4, 4, torch.device("cpu"))
+
+
+def test_plan_class_metadata_matches_certificates() -> None:
+    from rdna3_fastmm.schemes import load_scheme
+
+    for plan_type in (Rank7Plan, Rank48Plan, Rank49Plan):
+        scheme = load_scheme(plan_type.scheme_key)
+        assert (plan_type.rank, plan_type.scheme_size) == (scheme.rank, scheme.size)
+        assert plan_type.algorithm == scheme.algorithm
+
+
+def test_byte_formulas_and_precision_pairs(monkeypatch) -> None:
+    """reference test_rdna3.py:428-430, 520-522 (no allocation needed)."""
+    configure_supported_runtime(monkeypatch)
+    plan = Rank48Plan(257, 263, 269, torch.device("cuda", 0), dtype=torch.bfloat16, compute_dtype=torch.float16)
+    assert plan.workspace_bytes == 48 * (65 * 66 + 66 * 68 + 65 * 68) * 2
+    assert plan.prepacked_workspace_bytes == 48 * (65 * 66 + 65 * 68) * 2
+    assert plan.packed_weight_bytes == 48 * 66 * 68 * 2
+    rank49 = Rank49Plan(5, 6, 7, torch.device("cuda"))
+    assert rank49.workspace_bytes == 3 * 49 * 2 * 2 * 2
+    assert rank49.prepacked_workspace_bytes == 2 * 49 * 2 * 2 * 2
+    assert rank49.packed_right_bytes == 49 * 2 * 2 * 2
+    with pytest.raises(ValueError, match="does not support"):
+        Rank48Plan(8, 8, 8, torch.device("cuda"), dtype=torch.float16)
+    with pytest.raises(ValueError, match="does not support"):
+        Rank7Plan(8, 8, 8, torch.device("cuda"), dtype=torch.bfloat16, compute_dtype=torch.bfloat16)
+
+
+def test_memory_budget_is_checked_before_allocation(monkeypatch) -> None:
+    configure_supported_runtime(monkeypatch)
+    monkeypatch.setattr(torch.cuda, "mem_get_info", lambda device=None: (1 << 28, 1 << 38))
+    plan = Rank7Plan(8192, 8192, 8192, torch.device("cuda"), dtype=torch.bfloat16, compute_dtype=torch.float16)
+    with pytest.raises(MemoryError, match="budget"):
+        plan.allocate_workspace()
+    with pytest.raises(ValueError, match="interval"):
+        plan.allocate_workspace(max_free_memory_fraction=0)
+
+
+def test_measured_families_semantics(monkeypatch) -> None:
+    """reference test_rdna3.py:152-288: row interval x exact (K, N) x bias; prepacked adds families."""
+    monkeypatch.setattr(Rank7Plan, "linear_shape_families", (LinearShapeFamily(3_328, 9_216, 4_608, 12_288, False),))
+    monkeypatch.setattr(Rank7Plan, "prepacked_linear_shape_families", (LinearShapeFamily(720, 720, 4_096, 16_384, True),))
+    assert Rank7Plan.has_measured_linear_win((3_328, 4_608, 12_288), has_bias=False)
+    assert Rank7Plan.has_measured_linear_win((9_216, 4_608, 12_288), has_bias=False)
+    assert not Rank7Plan.has_measured_linear_win((9_217, 4_608, 12_288), has_bias=False)
+    assert not Rank7Plan.has_measured_linear_win((4_000, 4_608, 12_288), has_bias=True)
+    assert not Rank7Plan.has_measured_linear_win((720, 4_096, 16_384), has_bias=True)
+    assert Rank7Plan.has_measured_linear_win((720, 4_096, 16_384), has_bias=True, prepacked_weight=True)
+    assert not Rank7Plan.has_measured_linear_win((720, 4_096, 16_384), has_bias=False, prepacked_weight=True)
+
+
+def test_dispatch_tables_hold_only_measured_wins() -> None:
+    """Every family in the shipped tables must name a measured MI355X win (see MEASURED_WINS)."""
+    for plan_type in (Rank7Plan, Rank48Plan, Rank49Plan):
+        for family in plan_type.linear_shape_families + plan_type.prepacked_linear_shape_families:
+            assert family in runtime.MEASURED_WINS, (plan_type.__name__, family)
+
+
+def test_transform_config_reports_launch_geometry() -> None:
+    assert Rank7Plan.transform_config(4_096, 12_288).block_elements == 256 * 8
+    assert Rank48Plan.transform_config(8_192, 8_192).block_elements == 256 * 4
+    assert Rank49Plan.transform_config(263, 269).block_elements == 256
