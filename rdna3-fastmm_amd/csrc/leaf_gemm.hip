@@ -31,6 +31,9 @@
 // writes spread over all 64 banks) and leave as coalesced 16-byte row
 // segments.
 //
+// When Kb % 128 == 0 a 16x16x32 variant of the fast kernel (below, with its
+// own notes) runs instead; the 32x32x16 kernel covers the other fast shapes.
+//
 // Generic kernel (any Kb, any alignment): 256 x 256 tile, BK = 64, register-
 // staged loads with zero fill, double-buffered LDS; used for small or ragged
 // shapes where the fast kernel's preconditions fail.
@@ -274,6 +277,270 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
 
 }  // namespace fast
 
+// ------------------------------------------------------- 16x16x32 fast path
+
+// Main kernel for Kb % 128 == 0. Same 256 x 256 workgroup tile, 4 waves of
+// 128 x 128, 4-slot LDS ring of 32-wide K slices and 64-bank swizzle as the
+// kernel above, but on v_mfma_f32_16x16x32_f16: each wave holds 8 x 8
+// accumulators of 4 floats (256 AGPRs), one MFMA step consumes a whole slice,
+// and per slice and wave 64 MFMAs carry 16 fragment reads (one per 4 MFMAs,
+// for the next slice) and 8 ring refills (one per 8 MFMAs, four slices ahead).
+// On MI355X the MFMA rate of this GEMM is limited by board power, not by issue
+// slots: with random FP16 operands 16x16x32 sustains ~15 % more flop/s than
+// 32x32x16 at the same power, and spreading the refills over the whole slice
+// keeps the texture path from stalling the in-order MFMA issue.
+//
+// A slot is refilled as soon as its fragments are in registers: at the barrier
+// that opens slice kt every wave has waited for its reads of slice kt's slot
+// (issued during slice kt - 1), so that slot takes slice kt + 4 while slices
+// kt + 2 and kt + 3 are still in flight and slice kt + 1 is resident.
+//
+// The main loop is written as inline asm (MFMAs, fragment reads, waits) in
+// program order; the compiler's scheduler otherwise regroups the loads and
+// reads around the barrier. The asm operands tie every fragment to one of two
+// register sets, so no read overwrites a register an in-flight MFMA still
+// sources; s_nops before the epilogue cover the MFMA-to-AGPR-read latency the
+// compiler cannot see through the asm. Loads are buffer loads to LDS whose
+// range check (num_records = the leaf's bytes) drops rows past the leaf.
+//
+// Fragment layout (16x16x32, operands passed as (B', A')): lane l supplies
+// B'[n l%16][k 8*(l/16) .. +7] and A'[m l%16][same k]; accumulator element e
+// of lane l is P[m l%16][n 4*(l/16) + e].
+
+namespace mfma16 {
+
+constexpr int BK = 32;
+constexpr int STAGES = 4;
+constexpr int STAGE_HALVES = 2 * kTile * BK;
+constexpr int SEGMENTS = kTile / 16 / 4;
+constexpr int FM = 8, FN = 8;  // 16x16 accumulators per wave (128 x 128)
+constexpr int LDS_BYTES = fast::LDS_BYTES;
+static_assert(STAGES * STAGE_HALVES * 2 <= LDS_BYTES, "ring must fit the LDS reservation");
+
+typedef float float4v __attribute__((ext_vector_type(4)));
+using fast::lds_ptr;
+using fast::wait_vmcnt;
+
+template <int V>
+using Int = std::integral_constant<int, V>;
+template <bool V>
+using Bool = std::integral_constant<bool, V>;
+
+template <int kOut>
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B,
+                      void* __restrict__ P, int Mb, int Nb, int Kb, int tiles_m, int tiles_n,
+                      int total_tiles) {
+  extern __shared__ __attribute__((aligned(16))) half_t smem[];
+  int leaf, tm, tn;
+  decode_tile(blockIdx.x, total_tiles, tiles_m, tiles_n, 8, leaf, tm, tn);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int m0 = tm * kTile, n0 = tn * kTile;
+  const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<half_t*>(A + static_cast<int64_t>(leaf) * Mb * Kb), 0, Mb * Kb * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<half_t*>(B + static_cast<int64_t>(leaf) * Nb * Kb), 0, Nb * Kb * 2, 0x00020000);
+
+  // DMA mapping as in the 32x32 kernel: lane L of segment q writes row
+  // 16*(4q + wave) + L/4, physical chunk L%4, and fetches the logical chunk
+  // stored there. Byte offsets; rows past the leaf fail the range check.
+  const int seg_row = lane >> 2;
+  unsigned a_off[SEGMENTS], b_off[SEGMENTS];
+#pragma unroll
+  for (int q = 0; q < SEGMENTS; ++q) {
+    const int row = (q * 4 + wave) * 16 + seg_row;
+    const int chunk = (lane & 3) ^ ((row >> 2) & 3);
+    a_off[q] = static_cast<unsigned>(((m0 + row) * Kb + chunk * 8) * 2);
+    b_off[q] = static_cast<unsigned>(((n0 + row) * Kb + chunk * 8) * 2);
+  }
+  // Fragment reads: row l%16 of a 16-row block, logical chunk l/16. Two base
+  // addresses (slots {0,1} and {2,3}) keep every offset an immediate.
+  const int fr = lane & 15, fc = lane >> 4;
+  const int rd = fr * BK + ((fc ^ ((fr >> 2) & 3)) << 3);
+  unsigned base_a[2], base_b[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    // address-space casts: generic -> LDS pointer -> 32-bit LDS byte address
+    base_a[h] = (unsigned)(uintptr_t)(lds_ptr)(smem + h * 2 * STAGE_HALVES + wm * 128 * BK + rd);
+    base_b[h] = (unsigned)(uintptr_t)(lds_ptr)(smem + h * 2 * STAGE_HALVES + kTile * BK + wn * 128 * BK + rd);
+  }
+
+  half8 fa[2][FM], fb[2][FN];
+  float4v acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[i][j][e] = 0.0f;
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      fa[s][i] = half8{};
+      fb[s][i] = half8{};
+    }
+
+  // idx 0..3: A' segments, 4..7: B' segments of slice kt into ring slot `slot`
+  auto load_one = [&](int kt, int slot, int idx) {
+    const bool b_side = idx >= 4;
+    const int q = idx & 3;
+    half_t* dst = smem + slot * STAGE_HALVES + (b_side ? kTile * BK : 0) + (q * 4 + wave) * 16 * BK;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(b_side ? b_rsrc : a_rsrc, (lds_ptr)(dst), 16,
+                                             b_side ? b_off[q] : a_off[q], kt * BK * 2, 0, 0);
+  };
+#define FASTMM_READ(kSlotSrc, kSet, r)                                                              \
+  do {                                                                                              \
+    if constexpr ((r) < 8)                                                                          \
+      asm volatile("ds_read_b128 %0, %1 offset:%2"                                                  \
+                   : "+v"(fa[kSet][(r)])                                                            \
+                   : "v"(base_a[(kSlotSrc) / 2]), "i"((((kSlotSrc) % 2) * STAGE_HALVES + (r) * 16 * BK) * 2)); \
+    else                                                                                            \
+      asm volatile("ds_read_b128 %0, %1 offset:%2"                                                  \
+                   : "+v"(fb[kSet][(r) - 8])                                                        \
+                   : "v"(base_b[(kSlotSrc) / 2]),                                                   \
+                     "i"((((kSlotSrc) % 2) * STAGE_HALVES + ((r) - 8) * 16 * BK) * 2));             \
+  } while (0)
+#define FASTMM_MFMA(kSet, q)                                                                        \
+  asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0"                                             \
+               : "+a"(acc[(q) / 8][(q) % 8])                                                        \
+               : "v"(fb[kSet][(q) % 8]), "v"(fa[kSet][(q) / 8]))
+  // 4 MFMAs with one fragment read for the next slice; a refill after every other group
+#define FASTMM_GROUP(g)                                                                             \
+  do {                                                                                              \
+    FASTMM_MFMA(kSet, 4 * (g));                                                                     \
+    FASTMM_MFMA(kSet, 4 * (g) + 1);                                                                 \
+    if constexpr (kNext) FASTMM_READ(kNextSlot, 1 - kSet, (g));                                     \
+    FASTMM_MFMA(kSet, 4 * (g) + 2);                                                                 \
+    FASTMM_MFMA(kSet, 4 * (g) + 3);                                                                 \
+    if constexpr (kLoad && (g) % 2 == 1) load_one(kt + 4, kSlot, (g) / 2);                          \
+  } while (0)
+#define FASTMM_TIE(i)                                                                               \
+  asm volatile("" : "+a"(acc[i][0]), "+a"(acc[i][1]), "+a"(acc[i][2]), "+a"(acc[i][3]),             \
+                    "+a"(acc[i][4]), "+a"(acc[i][5]), "+a"(acc[i][6]), "+a"(acc[i][7]))
+  // The compiler cannot see that an asm MFMA's result is still in flight, so an
+  // accumulator copy, spill or read it places right after one would see a stale
+  // value. A fence waits out the MFMA latency (24 wait states) and then claims
+  // to modify every accumulator, so no compiler access to them can move above
+  // it; fences close every main-loop iteration (where the allocator places loop
+  // exit and back-edge copies), every tail step and the K loop.
+  auto fence = [&]() {
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+    FASTMM_TIE(0); FASTMM_TIE(1); FASTMM_TIE(2); FASTMM_TIE(3);
+    FASTMM_TIE(4); FASTMM_TIE(5); FASTMM_TIE(6); FASTMM_TIE(7);
+  };
+
+  // Slice kt in ring slot kSlot, fragments in register set kSlot % 2.
+  // kLoad: slice kt + 4 exists; kNext: slice kt + 1 exists; kSync: slice kt + 2
+  // exists and must be resident before the barrier, with kWait loads (those of
+  // slices kt + 3 and kt + 4) allowed in flight.
+  auto step = [&](int kt, auto slot_tag, auto load_tag, auto next_tag, auto sync_tag, auto wait_tag) {
+    constexpr int kSlot = decltype(slot_tag)::value;
+    constexpr bool kLoad = decltype(load_tag)::value;
+    constexpr bool kNext = decltype(next_tag)::value;
+    constexpr bool kSync = decltype(sync_tag)::value;
+    constexpr int kWait = decltype(wait_tag)::value;
+    constexpr int kSet = kSlot % 2, kNextSlot = (kSlot + 1) % STAGES;
+    FASTMM_GROUP(0); FASTMM_GROUP(1); FASTMM_GROUP(2); FASTMM_GROUP(3);
+    FASTMM_GROUP(4); FASTMM_GROUP(5); FASTMM_GROUP(6); FASTMM_GROUP(7);
+    FASTMM_GROUP(8); FASTMM_GROUP(9); FASTMM_GROUP(10); FASTMM_GROUP(11);
+    FASTMM_GROUP(12); FASTMM_GROUP(13); FASTMM_GROUP(14); FASTMM_GROUP(15);
+    if constexpr (kSync) wait_vmcnt<kWait>();
+    if constexpr (kNext) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if constexpr (kSync) fast::barrier();
+  };
+
+  const int nk = Kb / BK;  // multiple of 4, checked by the launcher
+#pragma unroll
+  for (int s = 0; s < STAGES; ++s)
+#pragma unroll
+    for (int idx = 0; idx < 8; ++idx) load_one(s, s, idx);
+  wait_vmcnt<16>();  // slices 0 and 1 resident
+  fast::barrier();
+  {
+    constexpr int kSrc = 0, kDst = 0;
+    FASTMM_READ(kSrc, kDst, 0); FASTMM_READ(kSrc, kDst, 1); FASTMM_READ(kSrc, kDst, 2); FASTMM_READ(kSrc, kDst, 3);
+    FASTMM_READ(kSrc, kDst, 4); FASTMM_READ(kSrc, kDst, 5); FASTMM_READ(kSrc, kDst, 6); FASTMM_READ(kSrc, kDst, 7);
+    FASTMM_READ(kSrc, kDst, 8); FASTMM_READ(kSrc, kDst, 9); FASTMM_READ(kSrc, kDst, 10); FASTMM_READ(kSrc, kDst, 11);
+    FASTMM_READ(kSrc, kDst, 12); FASTMM_READ(kSrc, kDst, 13); FASTMM_READ(kSrc, kDst, 14); FASTMM_READ(kSrc, kDst, 15);
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  fast::barrier();  // every wave holds slice 0: slot 0 may be refilled
+  asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");  // accumulator writes before the first MFMA
+  int kt = 0;
+  for (; kt < nk - 4; kt += 4) {
+    step(kt, Int<0>{}, Bool<true>{}, Bool<true>{}, Bool<true>{}, Int<16>{});
+    step(kt + 1, Int<1>{}, Bool<true>{}, Bool<true>{}, Bool<true>{}, Int<16>{});
+    step(kt + 2, Int<2>{}, Bool<true>{}, Bool<true>{}, Bool<true>{}, Int<16>{});
+    step(kt + 3, Int<3>{}, Bool<true>{}, Bool<true>{}, Bool<true>{}, Int<16>{});
+    fence();
+  }
+  step(kt, Int<0>{}, Bool<false>{}, Bool<true>{}, Bool<true>{}, Int<8>{});
+  fence();
+  step(kt + 1, Int<1>{}, Bool<false>{}, Bool<true>{}, Bool<true>{}, Int<0>{});
+  fence();
+  step(kt + 2, Int<2>{}, Bool<false>{}, Bool<true>{}, Bool<false>{}, Int<0>{});
+  fence();
+  step(kt + 3, Int<3>{}, Bool<false>{}, Bool<false>{}, Bool<false>{}, Int<0>{});
+  fence();
+#undef FASTMM_READ
+#undef FASTMM_MFMA
+#undef FASTMM_GROUP
+#undef FASTMM_TIE
+
+  const int64_t leaf_offset = static_cast<int64_t>(leaf) * Mb * Nb;
+  if constexpr (kOut == kFP32) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int row = m0 + wm * 128 + i * 16 + fr;
+      if (row >= Mb) continue;
+      float* out_row = static_cast<float*>(P) + leaf_offset + static_cast<int64_t>(row) * Nb;
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int col = n0 + wn * 128 + j * 16 + 4 * fc;
+        if (col < Nb) {
+          *reinterpret_cast<float4*>(out_row + col) =
+              make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+        }
+      }
+    }
+  } else {
+    // Stage the 256 x 256 fp16 tile in LDS (8-byte writes: 32 lanes cover all
+    // 64 banks at row pitch 264 halves), then store 16-byte row segments.
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    uint16_t* staged = reinterpret_cast<uint16_t*>(smem);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int row = wm * 128 + i * 16 + fr;
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int col = wn * 128 + j * 16 + 4 * fc;
+        uint16_t h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = f32_to_fp16(acc[i][j][e]);
+        store16<4>(staged + row * fast::OUT_PITCH + col, h);
+      }
+    }
+    __syncthreads();
+    const int chunk = tid & 31;
+    uint16_t* out = static_cast<uint16_t*>(P) + leaf_offset;
+#pragma unroll 4
+    for (int pass = 0; pass < kTile / 8; ++pass) {
+      const int row = pass * 8 + (tid >> 5);
+      const int grow = m0 + row, gcol = n0 + chunk * 8;
+      if (grow < Mb && gcol < Nb) {
+        uint16_t h[8];
+        load16<8>(staged + row * fast::OUT_PITCH + chunk * 8, h);
+        store16<8>(out + static_cast<int64_t>(grow) * Nb + gcol, h);
+      }
+    }
+  }
+}
+
+}  // namespace mfma16
+
 // -------------------------------------------------------------- generic path
 
 namespace generic {
@@ -423,12 +690,19 @@ int launch_tiles(Kernel kernel, int lds_bytes, const void* a, const void* b, voi
   return check_launch("leaf products");
 }
 
-// The fast kernel's preconditions; the generic kernel handles everything else.
+// The fast kernels' preconditions; the generic kernel handles everything else.
 bool fast_leaf_gemm_applies(const void* a, const void* b, const void* p, int64_t kb, int64_t nb,
                             int products_dtype) {
   const int64_t out_align = products_dtype == kFP32 ? 4 : 8;
   return kb % fast::BK == 0 && kb >= 3 * fast::BK && nb % out_align == 0 && aligned_to(a, 16) &&
          aligned_to(b, 16) && aligned_to(p, 16);
+}
+
+// The 16x16x32 kernel additionally needs whole groups of four slices and leaf
+// planes whose byte offsets fit its 32-bit buffer addressing.
+bool mfma16_leaf_gemm_applies(int64_t mb, int64_t kb, int64_t nb) {
+  return kb % (4 * mfma16::BK) == 0 && (mb + kTile) * kb * 2 <= INT32_MAX &&
+         (nb + kTile) * kb * 2 <= INT32_MAX;
 }
 
 }  // namespace fastmm
@@ -458,6 +732,12 @@ extern "C" int fastmm_leaf_products(int rank, const void* left_transformed,
   const void* b = right_transformed;
   void* p = products;
   const int64_t mb = block_rows, kb = block_inner, nb = block_columns;
+  if (fast_leaf_gemm_applies(a, b, p, kb, nb, products_dtype) && mfma16_leaf_gemm_applies(mb, kb, nb)) {
+    if (products_dtype == kFP32) {
+      return launch_tiles(mfma16::leaf_gemm_kernel<kFP32>, mfma16::LDS_BYTES, a, b, p, rank, mb, kb, nb, s);
+    }
+    return launch_tiles(mfma16::leaf_gemm_kernel<kFP16>, mfma16::LDS_BYTES, a, b, p, rank, mb, kb, nb, s);
+  }
   if (fast_leaf_gemm_applies(a, b, p, kb, nb, products_dtype)) {
     if (products_dtype == kFP32) {
       return launch_tiles(fast::leaf_gemm_kernel<kFP32>, fast::LDS_BYTES, a, b, p, rank, mb, kb, nb, s);

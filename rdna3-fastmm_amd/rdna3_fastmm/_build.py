@@ -5,6 +5,12 @@ nothing: the per-scheme programs in ``csrc/generated`` are checked in and a
 test keeps them equal to the generator's output. Every source is compiled
 with ``-ffp-contract=off`` (the transforms must round exactly like the fp32
 straight-line programs) and without packed-fp32 instructions.
+
+The 16x16x32 leaf-GEMM kernels issue their MFMAs as inline asm, whose result
+latency the compiler cannot see. The build therefore also emits the device
+assembly of ``leaf_gemm.hip`` and refuses to produce the library if any
+compiler-generated instruction touches an accumulator register written by an
+asm MFMA before a fence (three ``s_nop 7``) has covered its latency.
 """
 
 from __future__ import annotations
@@ -12,6 +18,7 @@ from __future__ import annotations
 from concurrent.futures import ThreadPoolExecutor
 import os
 from pathlib import Path
+import re
 import shutil
 import subprocess
 import sys
@@ -55,12 +62,81 @@ def _compile(source: str) -> Path:
     return target
 
 
+ASM_CHECKED_SOURCE = "leaf_gemm.hip"
+ASM_CHECKED_KERNELS = re.compile(r"^(_ZN6fastmm6mfma16\S*):", re.MULTILINE)
+_AGPR = re.compile(r"\ba(?:\[(\d+):(\d+)\]|(\d+)\b)")
+
+
+def _agprs(operands: str) -> set[int]:
+    registers: set[int] = set()
+    for low, high, single in _AGPR.findall(operands):
+        if single:
+            registers.add(int(single))
+        else:
+            registers.update(range(int(low), int(high) + 1))
+    return registers
+
+
+def fence_violations(assembly: str) -> list[str]:
+    """Instructions that touch an asm MFMA's accumulator before a fence.
+
+    Scans each ``fastmm::mfma16`` kernel in program order: an MFMA marks its
+    destination AGPRs pending; three consecutive ``s_nop 7`` (the fence's 24
+    wait states) clear them; any other instruction naming a pending AGPR is a
+    violation. Branches are followed in layout order, which covers the loop
+    body, its exit and the straight-line tail the compiler emits.
+    """
+    violations: list[str] = []
+    for match in ASM_CHECKED_KERNELS.finditer(assembly):
+        name = match.group(1)
+        body = assembly[match.end():]
+        body = body[: body.find("s_endpgm")]
+        pending: set[int] = set()
+        nops = 0
+        for line in body.splitlines():
+            text = line.split(";", 1)[0].strip()
+            if not text or text.endswith(":") or text.startswith("."):
+                continue
+            opcode, _, operands = text.partition(" ")
+            if opcode.startswith("v_mfma"):
+                destination = operands.split(",", 1)[0]
+                pending |= _agprs(destination)
+                nops = 0
+                continue
+            if opcode == "s_nop":
+                nops = nops + 1 if operands.strip() == "7" else 0
+                if nops >= 3:
+                    pending.clear()
+                continue
+            nops = 0
+            if pending & _agprs(operands):
+                violations.append(f"{name}: {text}")
+    return violations
+
+
+def _check_device_assembly() -> None:
+    target = BUILD_DIR / (Path(ASM_CHECKED_SOURCE).stem + ".s")
+    command = [_hipcc(), *COMMON_FLAGS, "--cuda-device-only", "-S", str(SOURCE_DIR / ASM_CHECKED_SOURCE), "-o", str(target)]
+    result = subprocess.run(command, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"assembling {ASM_CHECKED_SOURCE} failed:\n{result.stderr}")
+    assembly = target.read_text()
+    if not ASM_CHECKED_KERNELS.search(assembly):
+        raise RuntimeError(f"{ASM_CHECKED_SOURCE}: no mfma16 kernels found to check")
+    violations = fence_violations(assembly)
+    if violations:
+        listing = "\n".join(violations[:20])
+        raise RuntimeError(f"{ASM_CHECKED_SOURCE}: accumulator accessed inside MFMA latency:\n{listing}")
+
+
 def build_library(verbose: bool = False) -> Path:
-    """Compile every source and link the shared library; returns its path."""
+    """Compile every source, check the leaf-GEMM assembly, link; returns the path."""
     BUILD_DIR.mkdir(exist_ok=True)
-    workers = min(len(SOURCES), max(1, (os.cpu_count() or 2) // 2))
+    workers = min(len(SOURCES) + 1, max(1, (os.cpu_count() or 2) // 2))
     with ThreadPoolExecutor(max_workers=workers) as pool:
+        checked = pool.submit(_check_device_assembly)
         objects = list(pool.map(_compile, SOURCES))
+        checked.result()
     temporary = LIBRARY_PATH.with_suffix(".so.tmp")
     command = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(temporary)]
     result = subprocess.run(command, capture_output=True, text=True)

@@ -108,8 +108,12 @@ def test_reconstruct_bit_exact(key, shape, product_dtype) -> None:
     (
         # generic kernel: ragged or short K, unaligned rows
         (1, 5, 3, 7), (7, 33, 17, 129), (3, 256, 256, 64), (2, 300, 260, 136), (7, 129, 385, 2048), (5, 64, 64, 13),
-        # fast kernel: Kb % 32 == 0 and Kb >= 96, ragged Mb / Nb tails, one and many K slices
-        (2, 300, 264, 96), (3, 513, 520, 128), (7, 256, 256, 2048), (1, 4107, 16, 192), (2, 40, 8, 3072),
+        # 32x32x16 kernel: Kb % 32 == 0, Kb >= 96, Kb % 128 != 0
+        (2, 300, 264, 96), (1, 4107, 16, 192), (3, 129, 72, 224), (2, 256, 256, 1056),
+        # 16x16x32 kernel: Kb % 128 == 0 -- four slices only (no main-loop pass), one and
+        # several passes, ragged Mb / Nb tails, a single 8-column tile, rows not a multiple of 16
+        (3, 513, 520, 128), (2, 17, 24, 256), (7, 256, 256, 2048), (2, 40, 8, 3072), (1, 1000, 776, 640),
+        (4, 255, 264, 512),
     ),
 )
 @pytest.mark.parametrize("product_dtype", (torch.float16, torch.float32))

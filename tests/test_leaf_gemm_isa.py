@@ -1,0 +1,85 @@
+"""Static checks of the 16x16x32 leaf-GEMM kernels' gfx950 assembly (CPU only).
+
+The kernels issue their MFMAs as inline asm, so the compiler cannot see the
+MFMA result latency; correctness then rests on no compiler-generated
+instruction touching an accumulator inside that latency. These tests compile
+``leaf_gemm.hip`` to device assembly with the library's own flags and check
+that invariant (and that the checker catches a planted violation), plus the
+shape of the main loop that the kernel's throughput depends on.
+"""
+
+from __future__ import annotations
+
+import re
+import subprocess
+
+import pytest
+
+from rdna3_fastmm import _build
+
+
+@pytest.fixture(scope="module")
+def assembly(tmp_path_factory) -> str:
+    target = tmp_path_factory.mktemp("isa") / "leaf_gemm.s"
+    command = [
+        _build._hipcc(), *_build.COMMON_FLAGS, "--cuda-device-only", "-S",
+        str(_build.SOURCE_DIR / "leaf_gemm.hip"), "-o", str(target),
+    ]
+    result = subprocess.run(command, capture_output=True, text=True)
+    assert result.returncode == 0, result.stderr
+    return target.read_text()
+
+
+def _kernels(assembly: str) -> dict[str, str]:
+    bodies = {}
+    for match in _build.ASM_CHECKED_KERNELS.finditer(assembly):
+        body = assembly[match.end():]
+        bodies[match.group(1)] = body[: body.find("s_endpgm")]
+    return bodies
+
+
+def test_both_output_variants_are_checked(assembly) -> None:
+    names = _kernels(assembly)
+    assert any("ILi1E" in n for n in names) and any("ILi2E" in n for n in names), names
+
+
+def test_no_accumulator_access_inside_mfma_latency(assembly) -> None:
+    assert _build.fence_violations(assembly) == []
+
+
+def test_checker_reports_a_missing_fence(assembly) -> None:
+    # with the fences' nops shortened every epilogue read becomes a violation
+    planted = assembly.replace("s_nop 7", "s_nop 6")
+    assert len(_build.fence_violations(planted)) > 100
+
+
+def test_checker_on_synthetic_listing() -> None:
+    body = (
+        "_ZN6fastmm6mfma16kE:\n"
+        "\tv_mfma_f32_16x16x32_f16 a[0:3], v[0:3], v[4:7], a[0:3]\n"
+        "\tv_accvgpr_read_b32 v9, a4\n"  # other register: fine
+        "\tv_accvgpr_read_b32 v8, a2\n"  # inside the latency: violation
+        "\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n"
+        "\tv_accvgpr_read_b32 v8, a2\n"  # after a fence: fine
+        "\ts_endpgm\n"
+    )
+    assert _build.fence_violations(body) == ["_ZN6fastmm6mfma16kE: v_accvgpr_read_b32 v8, a2"]
+
+
+def test_main_loop_shape(assembly) -> None:
+    for name, body in _kernels(assembly).items():
+        loop = re.search(r"; =>This Inner Loop Header.*?s_cbranch_scc1", body, re.DOTALL)
+        assert loop, name
+        opcodes = [
+            line.split(";", 1)[0].split()[0]
+            for line in loop.group(0).splitlines()[1:]
+            if line.split(";", 1)[0].strip() and not line.strip().startswith(";")
+        ]
+        count = lambda prefix: sum(op.startswith(prefix) for op in opcodes)  # noqa: E731
+        # four slices per iteration: 64 MFMAs, 16 fragment reads, 8 refills each
+        assert count("v_mfma_f32_16x16x32_f16") == 256, name
+        assert count("ds_read_b128") == 64, name
+        assert count("buffer_load_dwordx4") == 32, name
+        assert count("s_barrier") == 4, name
+        for forbidden in ("v_accvgpr", "scratch_", "v_mov", "global_load", "flat_"):
+            assert count(forbidden) == 0, (name, forbidden)
