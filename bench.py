@@ -87,6 +87,14 @@ def _median(values: list[float]) -> float:
     return ordered[len(ordered) // 2]
 
 
+def leaf_kernel_name(block_inner: int) -> str:
+    """The leaf-GEMM kernel fastmm_leaf_products runs for the bench shapes (aligned
+    fp16 products): the 16x16x32 kernel when Kb % 128 == 0, else the 32x32x16 one."""
+    if block_inner % 128 == 0:
+        return "fastmm::mfma16::leaf_gemm_kernel<fp16> (fastmm_leaf_products)"
+    return "fastmm::fast::leaf_gemm_kernel<fp16> (fastmm_leaf_products)"
+
+
 def measured_traffic(config: str) -> float | None:
     """HBM-side bytes per leaf-GEMM launch from the committed rocprofv3 summary, if any.
 
@@ -293,7 +301,7 @@ def main() -> int:
         "stages_ms": {name: round(v, 4) for name, v in stage_ms.items()},
         "packing_ms": round(pack_ms, 4),
         "roofline": {
-            "kernel": "leaf_gemm_kernel (fastmm_leaf_products)",
+            "kernel": leaf_kernel_name(shape.block_inner),
             "bound": "mfma",
             "achieved": round(leaf_tflops, 2),
             "peak": MFMA_FP16_PEAK_TFLOPS,
