@@ -177,7 +177,7 @@ def main() -> int:
               file=sys.stderr)
         return 2
 
-    from rdna3_fastmm.runtime import PLAN_TYPES
+    from rdna3_fastmm.runtime import PLAN_TYPES, operand_shape
 
     cfg = CONFIGS[args.config]
     device = torch.device("cuda", 0)
@@ -240,7 +240,7 @@ def main() -> int:
     leaf_flops = 2.0 * plan.rank * shape.block_rows * shape.block_inner * shape.block_columns
     leaf_tflops = leaf_flops / (stage_ms["leaf_products"] * 1e-3) / 1e12
     pack_ms = _median(_event_ms(lambda: plan._transform_weight(w, workspace.products.new_empty(
-        (plan.rank, shape.block_columns, shape.block_inner))), 3))
+        operand_shape(plan.rank, shape.block_columns, shape.block_inner))), 3))
 
     # Accuracy on this workload (outside the timed region).
     if cfg["prepacked"]:

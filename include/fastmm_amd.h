@@ -24,12 +24,20 @@
  *   x / input      [rows, inner]            dtype (bf16 or fp16)
  *   weight         [columns, inner]         dtype  (F.linear layout)
  *   right          [inner, columns]         dtype  (mm path)
- *   left_transformed  A'[R, Mb, Kb]         fp16
- *   right_transformed B'[R, Nb, Kb]         fp16   (K-contiguous; the
+ *   left_transformed  A'[R, Mb, Kb]         fp16   (operand layout below)
+ *   right_transformed B'[R, Nb, Kb]         fp16   (operand layout below; the
  *        reference stores [R, Kb, Nb] and transposes inside torch.bmm)
- *   products       P[R, Mb, Nb]             fp16 or fp32
+ *   products       P[R, Mb, Nb]             fp16 or fp32, row-major
  *   bias           [columns]                dtype
  *   output         [rows, columns]          dtype
+ *
+ * Operand layout of A' and B' (same element count as [R, rows, Kb]): when
+ * Kb % 32 == 0 each plane is K-slab-major, element (row, k) at
+ *     ((k / 32) * rows + row) * 32 + k % 32        (rows = Mb or Nb),
+ * so the 32-wide K slice of a run of rows is contiguous; otherwise each plane
+ * is row-major, element (row, k) at row * Kb + k. The transforms write and
+ * fastmm_leaf_products reads this layout; buffers written by one library
+ * version are only valid for the same FASTMM_ABI_VERSION.
  */
 #ifndef FASTMM_AMD_H
 #define FASTMM_AMD_H
@@ -40,7 +48,7 @@
 extern "C" {
 #endif
 
-#define FASTMM_ABI_VERSION 1
+#define FASTMM_ABI_VERSION 2
 
 #define FASTMM_OK 0
 #define FASTMM_ERROR_ARGUMENT 1    /* bad pointer, size, dtype or scheme */

@@ -15,6 +15,25 @@ typedef float float16v __attribute__((ext_vector_type(16)));
 // Element codes shared with the C ABI (include/fastmm_amd.h).
 enum DType : int { kBF16 = 0, kFP16 = 1, kFP32 = 2 };
 
+// ---------------------------------------------------------- operand layout
+
+// Transformed operand planes (A' is [Mb, Kb], B' is [Nb, Kb]) are stored
+// K-slab-major when Kb is a multiple of 32: element (row, k) of a plane with
+// `rows` rows sits at ((k / 32) * rows + row) * 32 + k % 32, so the 32-wide K
+// slice of any run of rows is one contiguous block (a leaf-GEMM tile's slice
+// is 16 KB of consecutive bytes instead of 64-byte pieces of 256 rows). Other
+// Kb keep row-major planes.
+constexpr int kSlab = 32;
+
+__host__ __device__ __forceinline__ bool slab_layout(int64_t inner) { return inner % kSlab == 0; }
+
+template <bool kSlabLayout>
+__host__ __device__ __forceinline__ int64_t operand_offset(int64_t row, int64_t k, int64_t rows,
+                                                           int64_t inner) {
+  if constexpr (kSlabLayout) return ((k / kSlab) * rows + row) * kSlab + k % kSlab;
+  else return row * inner + k;
+}
+
 // ---------------------------------------------------------------- scalars
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t bits) {

@@ -1,6 +1,7 @@
 // Batched FP16 leaf products on CDNA4 MFMA (gfx950).
 //
-//   P[r] = A'[r] @ B'[r]^T,   A'[r]: [Mb, Kb], B'[r]: [Nb, Kb] (both K-contiguous)
+//   P[r] = A'[r] @ B'[r]^T,   A'[r]: [Mb, Kb], B'[r]: [Nb, Kb] in the operand layout of
+//   fastmm_device.h (K-slab-major when Kb % 32 == 0, else row-major); P row-major.
 //
 // Fast kernel (Kb % 32 == 0, Kb >= 96, 16-byte aligned operands): one
 // workgroup = 4 waves (one per SIMD) owns a 256 x 256 tile of one leaf; each
@@ -21,7 +22,8 @@
 // so the 16 lanes of one ds_read_b128 phase (16 consecutive rows, one k) hit 16
 // distinct (row % 4, chunk) bank groups; the DMA writes 1 KB contiguous per
 // instruction (lane L -> slot L), so the swizzle is applied by choosing which
-// global chunk each lane fetches.
+// global chunk each lane fetches. In the K-slab layout those 16 rows of one
+// slab are also 1 KB of consecutive global bytes.
 //
 // MFMA operands are passed as (B', A'): lane l supplies B'[n l%32][k 8*(l/32)
 // .. +7] and A'[m l%32][same k], so the accumulator holds P^T in the 32x32
@@ -108,16 +110,18 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
   const half_t* b_leaf = B + static_cast<int64_t>(leaf) * Nb * Kb;
 
   // DMA mapping: lane L of segment q writes row 16*q' + L/4, physical chunk L%4
-  // (q' = 4q + wave); it fetches the logical chunk stored there. Rows past the
-  // leaf are clamped onto its last row: they only feed outputs that are masked.
+  // (q' = 4q + wave); it fetches the logical chunk stored there. Operands are
+  // K-slab-major (Kb % 32 == 0), so a segment is 1 KB of consecutive bytes.
+  // Rows past the leaf are clamped onto its last row: they only feed outputs
+  // that are masked.
   const int seg_row = lane >> 2;
   int a_off[SEGMENTS], b_off[SEGMENTS];
 #pragma unroll
   for (int q = 0; q < SEGMENTS; ++q) {
     const int row = (q * 4 + wave) * 16 + seg_row;
     const int chunk = (lane & 3) ^ ((row >> 2) & 3);
-    a_off[q] = min(m0 + row, Mb - 1) * Kb + chunk * 8;
-    b_off[q] = min(n0 + row, Nb - 1) * Kb + chunk * 8;
+    a_off[q] = min(m0 + row, Mb - 1) * kSlab + chunk * 8;
+    b_off[q] = min(n0 + row, Nb - 1) * kSlab + chunk * 8;
   }
   const int lane_row = lane & 31, lane_half = lane >> 5;
   int rd_off[2];
@@ -139,15 +143,16 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
   auto load_slice = [&](int kt) {
     half_t* as = smem + (kt % STAGES) * STAGE_HALVES;
     half_t* bs = as + kTile * BK;
-    const int k0 = kt * BK;
+    const half_t* a_slab = a_leaf + static_cast<int64_t>(kt) * Mb * kSlab;
+    const half_t* b_slab = b_leaf + static_cast<int64_t>(kt) * Nb * kSlab;
 #pragma unroll
     for (int q = 0; q < SEGMENTS; ++q) {
-      __builtin_amdgcn_global_load_lds((global_ptr)(a_leaf + a_off[q] + k0),
+      __builtin_amdgcn_global_load_lds((global_ptr)(a_slab + a_off[q]),
                                        (lds_ptr)(as + (q * 4 + wave) * 16 * BK), 16, 0, 0);
     }
 #pragma unroll
     for (int q = 0; q < SEGMENTS; ++q) {
-      __builtin_amdgcn_global_load_lds((global_ptr)(b_leaf + b_off[q] + k0),
+      __builtin_amdgcn_global_load_lds((global_ptr)(b_slab + b_off[q]),
                                        (lds_ptr)(bs + (q * 4 + wave) * 16 * BK), 16, 0, 0);
     }
   };
@@ -300,8 +305,8 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
 // reads around the barrier. The asm operands tie every fragment to one of two
 // register sets, so no read overwrites a register an in-flight MFMA still
 // sources; s_nops before the epilogue cover the MFMA-to-AGPR-read latency the
-// compiler cannot see through the asm. Loads are buffer loads to LDS whose
-// range check (num_records = the leaf's bytes) drops rows past the leaf.
+// compiler cannot see through the asm. Loads are buffer loads to LDS from the
+// K-slab-major planes: a tile's slice is 16 KB of consecutive bytes.
 //
 // Fragment layout (16x16x32, operands passed as (B', A')): lane l supplies
 // B'[n l%16][k 8*(l/16) .. +7] and A'[m l%16][same k]; accumulator element e
@@ -345,15 +350,17 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
 
   // DMA mapping as in the 32x32 kernel: lane L of segment q writes row
   // 16*(4q + wave) + L/4, physical chunk L%4, and fetches the logical chunk
-  // stored there. Byte offsets; rows past the leaf fail the range check.
+  // stored there (byte offsets within a K slab; the slab is the scalar
+  // offset). Rows past the leaf are clamped onto its last row, so every
+  // address lies inside the leaf's planes.
   const int seg_row = lane >> 2;
   unsigned a_off[SEGMENTS], b_off[SEGMENTS];
 #pragma unroll
   for (int q = 0; q < SEGMENTS; ++q) {
     const int row = (q * 4 + wave) * 16 + seg_row;
     const int chunk = (lane & 3) ^ ((row >> 2) & 3);
-    a_off[q] = static_cast<unsigned>(((m0 + row) * Kb + chunk * 8) * 2);
-    b_off[q] = static_cast<unsigned>(((n0 + row) * Kb + chunk * 8) * 2);
+    a_off[q] = static_cast<unsigned>((min(m0 + row, Mb - 1) * kSlab + chunk * 8) * 2);
+    b_off[q] = static_cast<unsigned>((min(n0 + row, Nb - 1) * kSlab + chunk * 8) * 2);
   }
   // Fragment reads: row l%16 of a 16-row block, logical chunk l/16. Two base
   // addresses (slots {0,1} and {2,3}) keep every offset an immediate.
@@ -389,7 +396,8 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
     const int q = idx & 3;
     half_t* dst = smem + slot * STAGE_HALVES + (b_side ? kTile * BK : 0) + (q * 4 + wave) * 16 * BK;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(b_side ? b_rsrc : a_rsrc, (lds_ptr)(dst), 16,
-                                             b_side ? b_off[q] : a_off[q], kt * BK * 2, 0, 0);
+                                             b_side ? b_off[q] : a_off[q],
+                                             kt * (b_side ? Nb : Mb) * kSlab * 2, 0, 0);
   };
 #define FASTMM_READ(kSlotSrc, kSet, r)                                                              \
   do {                                                                                              \
@@ -555,7 +563,9 @@ __device__ __forceinline__ int swizzled(int row, int chunk) {
   return row * BK + ((chunk ^ (row & 7)) << 3);
 }
 
-template <bool kAligned, int kOut>
+// kSlabLayout: operand planes are K-slab-major (Kb % 32 == 0); a thread's 8
+// consecutive k stay inside one slab row.
+template <bool kAligned, int kOut, bool kSlabLayout>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B,
                       void* __restrict__ P, int Mb, int Nb, int Kb, int tiles_m, int tiles_n,
@@ -579,7 +589,7 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
       const int k = k0 + ((id & 7) << 3);
       uint4 v = make_uint4(0, 0, 0, 0);
       if (grow < rows) {
-        const half_t* p = base + static_cast<int64_t>(grow) * Kb + k;
+        const half_t* p = base + operand_offset<kSlabLayout>(grow, k, rows, Kb);
         if constexpr (kAligned) {
           if (k < Kb) v = *reinterpret_cast<const uint4*>(p);
         } else {
@@ -745,14 +755,20 @@ extern "C" int fastmm_leaf_products(int rank, const void* left_transformed,
     return launch_tiles(fast::leaf_gemm_kernel<kFP16>, fast::LDS_BYTES, a, b, p, rank, mb, kb, nb, s);
   }
   const bool aligned = kb % 8 == 0 && aligned_to(a, 16) && aligned_to(b, 16);
-  if (aligned) {
-    if (products_dtype == kFP32) {
-      return launch_tiles(generic::leaf_gemm_kernel<true, kFP32>, generic::LDS_BYTES, a, b, p, rank, mb, kb, nb, s);
-    }
-    return launch_tiles(generic::leaf_gemm_kernel<true, kFP16>, generic::LDS_BYTES, a, b, p, rank, mb, kb, nb, s);
+#define FASTMM_GENERIC(ALIGNED, SLAB)                                                                       \
+  do {                                                                                                      \
+    if (products_dtype == kFP32) {                                                                          \
+      return launch_tiles(generic::leaf_gemm_kernel<ALIGNED, kFP32, SLAB>, generic::LDS_BYTES, a, b, p,     \
+                          rank, mb, kb, nb, s);                                                             \
+    }                                                                                                       \
+    return launch_tiles(generic::leaf_gemm_kernel<ALIGNED, kFP16, SLAB>, generic::LDS_BYTES, a, b, p, rank, \
+                        mb, kb, nb, s);                                                                     \
+  } while (0)
+  if (slab_layout(kb)) {
+    if (aligned) FASTMM_GENERIC(true, true);
+    FASTMM_GENERIC(false, true);
   }
-  if (products_dtype == kFP32) {
-    return launch_tiles(generic::leaf_gemm_kernel<false, kFP32>, generic::LDS_BYTES, a, b, p, rank, mb, kb, nb, s);
-  }
-  return launch_tiles(generic::leaf_gemm_kernel<false, kFP16>, generic::LDS_BYTES, a, b, p, rank, mb, kb, nb, s);
+  if (aligned) FASTMM_GENERIC(true, false);
+  FASTMM_GENERIC(false, false);
+#undef FASTMM_GENERIC
 }

@@ -1,5 +1,8 @@
 // Block transforms and output recombination for every scheme (gfx950).
 //
+// Transformed planes are written in the operand layout of fastmm_device.h
+// (K-slab-major when Kb % 32 == 0, else row-major).
+//
 // All three kernels are HBM-bound elementwise passes over one block plane:
 // a thread owns EPT consecutive plane elements (K-contiguous for the
 // transforms, N-contiguous for the recombination), reads the s*s input
@@ -32,7 +35,9 @@ enum Side : int { kLeftSide = 0, kWeightSide = 1 };
 //         W[src_rows = N, src_cols = K]; plane r of B' is [Nb, Kb].
 // kVector: src_cols == s * cols_b, cols_b % EPT == 0 and 2*EPT-aligned
 // pointers, so every vector is wholly inside a row; otherwise EPT == 1.
-template <class S, int kSide, int kDType, int EPT, bool kVector>
+// kSlabLayout: output planes K-slab-major (cols_b % 32 == 0); a thread's EPT
+// elements stay inside one 32-wide slab row (EPT divides 32).
+template <class S, int kSide, int kDType, int EPT, bool kVector, bool kSlabLayout>
 __global__ __launch_bounds__(kThreads) void direct_transform_kernel(
     const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, int64_t src_rows,
     int64_t src_cols, int64_t rows_b, int64_t cols_b) {
@@ -40,8 +45,19 @@ __global__ __launch_bounds__(kThreads) void direct_transform_kernel(
   const int64_t plane = rows_b * cols_b;
   const int64_t first = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * EPT;
   if (first >= plane) return;
-  const int64_t row = first / cols_b;
-  const int64_t col = first - row * cols_b;
+  // Threads walk the output plane in storage order, so a wavefront's stores
+  // are one contiguous run; `first` is both the thread's output offset and,
+  // decoded, its (row, col) position.
+  int64_t row, col;
+  if constexpr (kSlabLayout) {
+    const int64_t slab = first / (rows_b * kSlab);
+    const int64_t within = first - slab * (rows_b * kSlab);
+    row = within / kSlab;
+    col = slab * kSlab + (within - row * kSlab);
+  } else {
+    row = first / cols_b;
+    col = first - row * cols_b;
+  }
 
   auto load = [&](int j) -> Vec<EPT> {
     const int block_row = kSide == kLeftSide ? j / s : j % s;
@@ -72,10 +88,12 @@ __global__ __launch_bounds__(kThreads) void direct_transform_kernel(
 
 // B' from a row-major right[K, N] (the mm path): the blocks are N-contiguous
 // in memory but B' planes are K-contiguous, so a 32x32 (k, n) tile of every
-// input block is staged through LDS and read transposed.
+// input block is staged through LDS and read transposed. In the K-slab
+// layout a tile's output is one contiguous 2 KB block per plane.
 constexpr int kTransposeTile = 32;
+static_assert(kTransposeTile == kSlab, "a transpose tile covers exactly one K slab");
 
-template <class S, int kDType>
+template <class S, int kDType, bool kSlabLayout>
 __global__ __launch_bounds__(kThreads) void transposed_right_kernel(
     const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, int64_t inner,
     int64_t columns, int64_t kb, int64_t nb) {
@@ -114,7 +132,7 @@ __global__ __launch_bounds__(kThreads) void transposed_right_kernel(
   const int64_t k = k0 + k_local;
   auto store = [&](int r, const Vec<4>& v) {
     if (n >= nb) return;
-    uint16_t* p = dst + (static_cast<int64_t>(r) * nb + n) * kb + k;
+    uint16_t* p = dst + static_cast<int64_t>(r) * nb * kb + operand_offset<kSlabLayout>(n, k, nb, kb);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       if (k + e < kb) p[e] = f32_to_fp16(v.v[e]);
@@ -204,14 +222,20 @@ int launch_direct(int side, int dtype, const void* src, void* dst, int64_t src_r
   const dim3 grid(static_cast<unsigned>(ceil_div(plane, per_block)));
   const uint16_t* in = static_cast<const uint16_t*>(src);
   uint16_t* out = static_cast<uint16_t*>(dst);
-#define FASTMM_DIRECT(SIDE, DT)                                                              \
+  const bool slab = slab_layout(cols_b);
+#define FASTMM_DIRECT_LAYOUT(SIDE, DT, SLAB)                                                 \
   do {                                                                                       \
     if (vector)                                                                              \
-      direct_transform_kernel<S, SIDE, DT, W, true>                                          \
+      direct_transform_kernel<S, SIDE, DT, W, true, SLAB>                                    \
           <<<grid, kThreads, 0, stream>>>(in, out, src_rows, src_cols, rows_b, cols_b);      \
     else                                                                                     \
-      direct_transform_kernel<S, SIDE, DT, 1, false>                                         \
+      direct_transform_kernel<S, SIDE, DT, 1, false, SLAB>                                   \
           <<<grid, kThreads, 0, stream>>>(in, out, src_rows, src_cols, rows_b, cols_b);      \
+  } while (0)
+#define FASTMM_DIRECT(SIDE, DT)                                                              \
+  do {                                                                                       \
+    if (slab) FASTMM_DIRECT_LAYOUT(SIDE, DT, true);                                          \
+    else FASTMM_DIRECT_LAYOUT(SIDE, DT, false);                                              \
   } while (0)
   if (side == kLeftSide) {
     if (dtype == kBF16) FASTMM_DIRECT(kLeftSide, kBF16);
@@ -221,6 +245,7 @@ int launch_direct(int side, int dtype, const void* src, void* dst, int64_t src_r
     else FASTMM_DIRECT(kWeightSide, kFP16);
   }
 #undef FASTMM_DIRECT
+#undef FASTMM_DIRECT_LAYOUT
   return check_launch(side == kLeftSide ? "left transform" : "weight transform");
 }
 
@@ -234,10 +259,13 @@ int launch_transposed(int dtype, const void* src, void* dst, int64_t inner, int6
                   static_cast<unsigned>(ceil_div(kb, kTransposeTile)));
   const uint16_t* in = static_cast<const uint16_t*>(src);
   uint16_t* out = static_cast<uint16_t*>(dst);
+  const bool slab = slab_layout(kb);
   if (dtype == kBF16) {
-    transposed_right_kernel<S, kBF16><<<grid, kThreads, 0, stream>>>(in, out, inner, columns, kb, nb);
+    if (slab) transposed_right_kernel<S, kBF16, true><<<grid, kThreads, 0, stream>>>(in, out, inner, columns, kb, nb);
+    else transposed_right_kernel<S, kBF16, false><<<grid, kThreads, 0, stream>>>(in, out, inner, columns, kb, nb);
   } else {
-    transposed_right_kernel<S, kFP16><<<grid, kThreads, 0, stream>>>(in, out, inner, columns, kb, nb);
+    if (slab) transposed_right_kernel<S, kFP16, true><<<grid, kThreads, 0, stream>>>(in, out, inner, columns, kb, nb);
+    else transposed_right_kernel<S, kFP16, false><<<grid, kThreads, 0, stream>>>(in, out, inner, columns, kb, nb);
   }
   return check_launch("right transform");
 }

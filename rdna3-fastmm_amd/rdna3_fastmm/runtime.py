@@ -11,9 +11,12 @@ plans keep no state besides the shape.
 
 Differences that are visible to a caller, all deliberate:
 
-* ``PackedWeight.transformed`` / ``Workspace.right_transformed`` hold B' as
-  ``[R, Nb, Kb]`` (K-contiguous, what the MFMA kernel reads) instead of the
-  reference's ``[R, Kb, Nb]``; both are opaque snapshots with the same bytes.
+* ``PackedWeight.transformed`` / ``Workspace.right_transformed`` hold B' and
+  ``Workspace.left_transformed`` holds A' in the layout the HIP kernels read
+  (``operand_shape``): K-slab-major ``[R, Kb/32, Nb, 32]`` when ``Kb % 32 == 0``,
+  else ``[R, Nb, Kb]`` -- instead of the reference's ``[R, Kb, Nb]``; the
+  element values are the reference's, only their order differs (opaque
+  snapshots either way).
 * The runtime gate accepts gfx950 with 256 CUs on the torch/ROCm build this
   package was measured with, and the measured-win tables below were derived on
   that GPU against native BF16 ``torch.mm``/``F.linear``.
@@ -32,6 +35,22 @@ from .schemes import Scheme, load_scheme
 
 def _ceil_div(a: int, b: int) -> int:
     return -(-a // b)
+
+
+SLAB_WIDTH = 32
+
+
+def operand_shape(rank: int, rows: int, inner: int) -> tuple[int, ...]:
+    """Buffer shape of a transformed operand (A': rows = Mb, B': rows = Nb).
+
+    When ``inner`` (Kb) is a multiple of 32 the planes are K-slab-major,
+    ``[R, Kb/32, rows, 32]``: the 32-wide K slice of any run of rows is
+    contiguous, which is how the leaf-GEMM kernels stream tiles. Otherwise
+    they are row-major ``[R, rows, Kb]``. Same element count either way.
+    """
+    if inner % SLAB_WIDTH == 0:
+        return (rank, inner // SLAB_WIDTH, rows, SLAB_WIDTH)
+    return (rank, rows, inner)
 
 
 @dataclass(frozen=True)
@@ -280,10 +299,10 @@ class _Plan:
             algorithm=self.algorithm,
             output_dtype=self.dtype,
             compute_dtype=self.compute_dtype,
-            left_transformed=self._empty((self.rank, shape.block_rows, shape.block_inner)),
+            left_transformed=self._empty(operand_shape(self.rank, shape.block_rows, shape.block_inner)),
             right_transformed=None
             if prepacked_right
-            else self._empty((self.rank, shape.block_columns, shape.block_inner)),
+            else self._empty(operand_shape(self.rank, shape.block_columns, shape.block_inner)),
             products=self._empty((self.rank, shape.block_rows, shape.block_columns)),
         )
 
@@ -296,7 +315,7 @@ class _Plan:
             self.packed_right_bytes, max_free_memory_fraction, f"{self.algorithm} packed right matrix"
         )
         shape = self.shape
-        transformed = self._empty((self.rank, shape.block_columns, shape.block_inner))
+        transformed = self._empty(operand_shape(self.rank, shape.block_columns, shape.block_inner))
         self._transform_right(right, transformed)
         return PackedRight(
             algorithm=self.algorithm,
@@ -408,14 +427,14 @@ class _Plan:
             raise ValueError("workspace does not match the plan")
         shape = self.shape
         expected = [
-            (workspace.left_transformed, (self.rank, shape.block_rows, shape.block_inner)),
+            (workspace.left_transformed, operand_shape(self.rank, shape.block_rows, shape.block_inner)),
             (workspace.products, (self.rank, shape.block_rows, shape.block_columns)),
         ]
         if require_right:
             if workspace.right_transformed is None:
                 raise ValueError("dynamic execution requires a dynamic workspace")
             expected.append(
-                (workspace.right_transformed, (self.rank, shape.block_columns, shape.block_inner))
+                (workspace.right_transformed, operand_shape(self.rank, shape.block_columns, shape.block_inner))
             )
         for tensor, tensor_shape in expected:
             if (
@@ -447,7 +466,7 @@ class _Plan:
         shape = self.shape
         transformed = packed.transformed
         if (
-            tuple(transformed.shape) != (self.rank, shape.block_columns, shape.block_inner)
+            tuple(transformed.shape) != operand_shape(self.rank, shape.block_columns, shape.block_inner)
             or transformed.device != self.device
             or transformed.dtype != self.compute_dtype
             or not transformed.is_contiguous()
@@ -538,7 +557,7 @@ class _LinearPlan(_Plan):
             self.packed_weight_bytes, max_free_memory_fraction, f"{self.algorithm} packed Linear weight"
         )
         shape = self.shape
-        transformed = self._empty((self.rank, shape.block_columns, shape.block_inner))
+        transformed = self._empty(operand_shape(self.rank, shape.block_columns, shape.block_inner))
         self._transform_weight(weight, transformed)
         return PackedWeight(
             algorithm=self.algorithm,

@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 import torch
 
+from _layout import from_operand
 from oracle import fastmm_oracle as O
 from rdna3_fastmm.linear import rdna3_linear, rdna3_rank7_linear, rdna3_rank48_linear
 from rdna3_fastmm.runtime import PLAN_TYPES, Rank7Plan, Rank48Plan, Rank49Plan
@@ -70,7 +71,14 @@ def test_linear_exact_small_integer_product(plan_type, shape) -> None:
 
 
 @pytest.mark.parametrize("plan_type", LINEAR_PLANS)
-def test_linear_matches_oracle_and_bounded_error(plan_type) -> None:
+@pytest.mark.parametrize(
+    "shape",
+    (
+        (257, 263, 269),  # ragged blocks, row-major operands, generic leaf kernel
+        (200, 512, 544),  # Kb % 128 == 0: K-slab operands and the 16x16x32 leaf kernel
+    ),
+)
+def test_linear_matches_oracle_and_bounded_error(plan_type, shape) -> None:
     """reference test_rdna3.py:487-613 at 257x263x269, plus the stage-by-stage oracle check.
 
     After a dynamic run the workspace holds every intermediate, so each stage
@@ -79,8 +87,7 @@ def test_linear_matches_oracle_and_bounded_error(plan_type) -> None:
     rounding), and the output bit-exact to the oracle's recombination of the
     GPU's own products.
     """
-    print(f"\n[case] bounded error {plan_type.__name__}", flush=True)
-    shape = (257, 263, 269)
+    print(f"\n[case] bounded error {plan_type.__name__} {shape}", flush=True)
     g = torch.Generator().manual_seed(17)
     x = torch.randn(shape[:2], generator=g).to(torch.bfloat16)
     w = torch.randn((shape[2], shape[1]), generator=g).to(torch.bfloat16)
@@ -94,8 +101,12 @@ def test_linear_matches_oracle_and_bounded_error(plan_type) -> None:
     oracle = O.load_oracle_scheme(plan.scheme_key)
     a = O.left_transform(oracle, x.float().numpy())
     b = O.weight_transform(oracle, w.float().numpy())
-    assert np.array_equal(workspace.left_transformed.cpu().numpy().view(np.int16), a.view(np.int16))
-    assert np.array_equal(workspace.right_transformed.cpu().numpy().view(np.int16), b.view(np.int16))
+    rank, mb, kb = a.shape
+    nb = b.shape[1]
+    left_bits = workspace.left_transformed.cpu().numpy().view(np.int16)
+    right_bits = workspace.right_transformed.cpu().numpy().view(np.int16)
+    assert np.array_equal(from_operand(left_bits, rank, mb, kb), a.view(np.int16))
+    assert np.array_equal(from_operand(right_bits, rank, nb, kb), b.view(np.int16))
     products = workspace.products.cpu().numpy()
     exact = O.leaf_products(a, b, product_dtype="fp32").astype(np.float64)
     magnitude = np.matmul(np.abs(a.astype(np.float64)), np.abs(np.swapaxes(b.astype(np.float64), 1, 2)))

@@ -1,7 +1,8 @@
 """Every HIP stage against the CPU oracle on the same seeded inputs.
 
 Transforms and recombination are bit-exact (same fp32 program order, same
-round-to-nearest-even stores). Leaf products differ from the oracle's
+round-to-nearest-even stores); transformed operands are compared in logical
+plane order after undoing the kernels' K-slab layout (``tests/_layout.py``). Leaf products differ from the oracle's
 near-exact fp64 sum only by fp32 accumulation: the bound below is the
 standard ``K * 2^-24 * sum|a*b|`` (plus one fp16 ulp when stored as fp16).
 """
@@ -10,8 +11,10 @@ import numpy as np
 import pytest
 import torch
 
+from _layout import from_operand, to_operand
 from oracle import fastmm_oracle as O
 from rdna3_fastmm import _stages
+from rdna3_fastmm.runtime import operand_shape
 from rdna3_fastmm.schemes import SCHEME_KEYS, load_scheme
 
 pytestmark = pytest.mark.gpu
@@ -60,8 +63,9 @@ def test_transforms_bit_exact(key, shape, dtype) -> None:
     s, r = scheme.size, scheme.rank
     x, w, _ = _inputs(shape, dtype, seed=m + k + n)
     xg, wg = x.to(DEVICE), w.to(DEVICE)
-    a = torch.empty((r, _ceil(m, s), _ceil(k, s)), device=DEVICE, dtype=torch.float16)
-    b = torch.empty((r, _ceil(n, s), _ceil(k, s)), device=DEVICE, dtype=torch.float16)
+    mb, kb, nb = _ceil(m, s), _ceil(k, s), _ceil(n, s)
+    a = torch.empty(operand_shape(r, mb, kb), device=DEVICE, dtype=torch.float16)
+    b = torch.empty(operand_shape(r, nb, kb), device=DEVICE, dtype=torch.float16)
     b2 = torch.empty_like(b)
     _stages.left_transform(scheme, xg, a, m, k)
     _stages.weight_transform(scheme, wg, b, n, k)
@@ -70,9 +74,9 @@ def test_transforms_bit_exact(key, shape, dtype) -> None:
     torch.cuda.synchronize()
     expect_a = O.left_transform(oracle, _np(x)).view(np.int16)
     expect_b = O.weight_transform(oracle, _np(w)).view(np.int16)
-    assert np.array_equal(_bits(a), expect_a)
-    assert np.array_equal(_bits(b), expect_b)
-    assert np.array_equal(_bits(b2), expect_b)
+    assert np.array_equal(from_operand(_bits(a), r, mb, kb), expect_a)
+    assert np.array_equal(from_operand(_bits(b), r, nb, kb), expect_b)
+    assert np.array_equal(from_operand(_bits(b2), r, nb, kb), expect_b)
 
 
 @pytest.mark.parametrize("key", SCHEME_KEYS)
@@ -124,7 +128,9 @@ def test_leaf_products_within_fp32_accumulation_bound(dims, product_dtype) -> No
     a = torch.randn((rank, mb, kb), generator=g).half()
     b = torch.randn((rank, nb, kb), generator=g).half()
     p = torch.empty((rank, mb, nb), device=DEVICE, dtype=product_dtype)
-    _stages.leaf_products(rank, a.to(DEVICE), b.to(DEVICE), p, mb, kb, nb)
+    a_dev = torch.from_numpy(to_operand(a.numpy())).to(DEVICE)
+    b_dev = torch.from_numpy(to_operand(b.numpy())).to(DEVICE)
+    _stages.leaf_products(rank, a_dev, b_dev, p, mb, kb, nb)
     torch.cuda.synchronize()
     exact = O.leaf_products(a.numpy(), b.numpy(), product_dtype="fp32")
     magnitude = np.matmul(np.abs(a.numpy().astype(np.float64)), np.abs(np.swapaxes(b.numpy().astype(np.float64), 1, 2)))

@@ -155,3 +155,28 @@ def test_transform_config_reports_launch_geometry() -> None:
     assert Rank7Plan.transform_config(4_096, 12_288).block_elements == 256 * 8
     assert Rank48Plan.transform_config(8_192, 8_192).block_elements == 256 * 4
     assert Rank49Plan.transform_config(263, 269).block_elements == 256
+
+
+def test_operand_layout_is_k_slab_major_exactly_when_kb_is_a_multiple_of_32() -> None:
+    """The documented index: element (row, k) of a plane at ((k // 32) * rows + row) * 32 + k % 32."""
+    import numpy as np
+
+    from _layout import from_operand, to_operand
+    from rdna3_fastmm.runtime import operand_shape
+
+    assert operand_shape(7, 100, 256) == (7, 8, 100, 32)
+    assert operand_shape(7, 100, 250) == (7, 100, 250)
+    assert operand_shape(48, 5, 32) == (48, 1, 5, 32)
+    rank, rows, inner = 3, 5, 64
+    planes = np.arange(rank * rows * inner).reshape(rank, rows, inner)
+    buffer = to_operand(planes)
+    assert buffer.shape == operand_shape(rank, rows, inner)
+    flat = buffer.reshape(rank, -1)
+    for r in range(rank):
+        for row in range(rows):
+            for k in range(inner):
+                assert flat[r, ((k // 32) * rows + row) * 32 + k % 32] == planes[r, row, k]
+    assert np.array_equal(from_operand(buffer, rank, rows, inner), planes)
+    ragged = np.arange(2 * 3 * 40).reshape(2, 3, 40)
+    assert np.array_equal(to_operand(ragged), ragged)
+    assert np.array_equal(from_operand(to_operand(ragged), 2, 3, 40), ragged)
