@@ -47,15 +47,19 @@ namespace fastmm {
 constexpr int kGemmThreads = 256;
 constexpr int kTile = 256;
 
-// Workgroups are dispatched round-robin over the 8 XCDs; renumber so that each
-// XCD works on a contiguous range of tiles (tiles of one leaf share A'/B' rows
-// in that XCD's L2), then walk the tiles of a leaf in groups of `group` tile
-// rows, column by column.
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup w runs on
+// XCD w % 8); renumber so that each XCD works on a contiguous range of tiles
+// (tiles of one leaf share A'/B' rows in that XCD's L2): with q = total / 8
+// and r = total % 8, XCD x receives q + 1 workgroups if x < r, else q, and
+// takes the logical tiles starting at x*(q+1) (x < r) or r*(q+1) + (x-r)*q.
+// Then walk the tiles of a leaf in groups of `group` tile rows, column by
+// column.
 __device__ __forceinline__ void decode_tile(int wg, int total, int tiles_m, int tiles_n,
                                             int group, int& leaf, int& tm, int& tn) {
   constexpr int kXcds = 8;
-  int logical = wg;
-  if (total % kXcds == 0) logical = (wg % kXcds) * (total / kXcds) + wg / kXcds;
+  const int q = total / kXcds, r = total - q * kXcds;
+  const int x = wg % kXcds, i = wg / kXcds;
+  const int logical = x < r ? x * (q + 1) + i : r * (q + 1) + (x - r) * q + i;
   const int per_leaf = tiles_m * tiles_n;
   leaf = logical / per_leaf;
   const int t = logical - leaf * per_leaf;
