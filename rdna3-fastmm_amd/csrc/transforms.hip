@@ -35,28 +35,31 @@ enum Side : int { kLeftSide = 0, kWeightSide = 1 };
 //         W[src_rows = N, src_cols = K]; plane r of B' is [Nb, Kb].
 // kVector: src_cols == s * cols_b, cols_b % EPT == 0 and 2*EPT-aligned
 // pointers, so every vector is wholly inside a row; otherwise EPT == 1.
-// kSlabLayout: output planes K-slab-major (cols_b % 32 == 0); a thread's EPT
-// elements stay inside one 32-wide slab row (EPT divides 32).
-template <class S, int kSide, int kDType, int EPT, bool kVector, bool kSlabLayout>
+// kSpan == 0: row-major output planes; a 1D grid walks them in storage order.
+// kSpan == 32 or 64: K-slab-major output planes (cols_b % kSpan == 0); a 2D
+// grid gives each wave RPW rows x kSpan columns, so a wave reads whole 64- or
+// 128-byte line runs of every input row and writes RPW consecutive slab rows
+// (RPW * 64 bytes) per slab and plane.
+template <class S, int kSide, int kDType, int EPT, bool kVector, int kSpan>
 __global__ __launch_bounds__(kThreads) void direct_transform_kernel(
     const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, int64_t src_rows,
     int64_t src_cols, int64_t rows_b, int64_t cols_b) {
   constexpr int s = S::kSize;
   const int64_t plane = rows_b * cols_b;
-  const int64_t first = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * EPT;
-  if (first >= plane) return;
-  // Threads walk the output plane in storage order, so a wavefront's stores
-  // are one contiguous run; `first` is both the thread's output offset and,
-  // decoded, its (row, col) position.
-  int64_t row, col;
-  if constexpr (kSlabLayout) {
-    const int64_t slab = first / (rows_b * kSlab);
-    const int64_t within = first - slab * (rows_b * kSlab);
-    row = within / kSlab;
-    col = slab * kSlab + (within - row * kSlab);
+  int64_t row, col, at;
+  if constexpr (kSpan == 0) {
+    at = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * EPT;
+    if (at >= plane) return;
+    row = at / cols_b;
+    col = at - row * cols_b;
   } else {
-    row = first / cols_b;
-    col = first - row * cols_b;
+    constexpr int CPR = kSpan / EPT, RPW = 64 / CPR;  // chunks per row, rows per wave
+    static_assert(CPR * RPW == 64 && kSpan % kSlab == 0, "a wave covers whole slab rows");
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    row = (static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + wave) * RPW + lane / CPR;
+    col = static_cast<int64_t>(blockIdx.y) * kSpan + (lane % CPR) * EPT;
+    if (row >= rows_b) return;
+    at = operand_offset<true>(row, col, rows_b, cols_b);
   }
 
   auto load = [&](int j) -> Vec<EPT> {
@@ -77,7 +80,7 @@ __global__ __launch_bounds__(kThreads) void direct_transform_kernel(
     }
   };
   auto store = [&](int k, const Vec<EPT>& v) {
-    store_vec<kFP16, EPT>(dst + k * plane + first, v);
+    store_vec<kFP16, EPT>(dst + k * plane + at, v);
   };
   if constexpr (kSide == kLeftSide) {
     S::template left<Vec<EPT>>(load, store);
@@ -218,24 +221,36 @@ int launch_direct(int side, int dtype, const void* src, void* dst, int64_t src_r
   const int64_t cols_b = ceil_div(src_cols, s);
   const bool vector = src_cols % (s * W) == 0 && aligned_to(src, 2 * W) && aligned_to(dst, 2 * W);
   const int64_t plane = rows_b * cols_b;
-  const int64_t per_block = static_cast<int64_t>(kThreads) * (vector ? W : 1);
-  const dim3 grid(static_cast<unsigned>(ceil_div(plane, per_block)));
   const uint16_t* in = static_cast<const uint16_t*>(src);
   uint16_t* out = static_cast<uint16_t*>(dst);
-  const bool slab = slab_layout(cols_b);
-#define FASTMM_DIRECT_LAYOUT(SIDE, DT, SLAB)                                                 \
+  const int span = !slab_layout(cols_b) ? 0 : cols_b % 64 == 0 ? 64 : 32;
+  if (span != 0 && cols_b / span > 65535) {
+    return fail(FASTMM_ERROR_UNSUPPORTED, "transform: inner dimension too large for the K-span grid");
+  }
+  // 1D grid over the plane (row-major) or 2D grid of (4 waves x RPW rows) x kSpan columns
+  auto grid_for = [&](int ept, int kspan) {
+    if (kspan == 0) return dim3(static_cast<unsigned>(ceil_div(plane, static_cast<int64_t>(kThreads) * ept)));
+    const int64_t rows_per_block = static_cast<int64_t>(kThreads / 64) * (64 / (kspan / ept));
+    return dim3(static_cast<unsigned>(ceil_div(rows_b, rows_per_block)), static_cast<unsigned>(cols_b / kspan));
+  };
+#define FASTMM_DIRECT_LAYOUT(SIDE, DT, SPAN)                                                 \
   do {                                                                                       \
     if (vector)                                                                              \
-      direct_transform_kernel<S, SIDE, DT, W, true, SLAB>                                    \
-          <<<grid, kThreads, 0, stream>>>(in, out, src_rows, src_cols, rows_b, cols_b);      \
+      direct_transform_kernel<S, SIDE, DT, W, true, SPAN><<<grid_for(W, SPAN), kThreads, 0,   \
+                                                             stream>>>(in, out, src_rows,    \
+                                                                       src_cols, rows_b,     \
+                                                                       cols_b);              \
     else                                                                                     \
-      direct_transform_kernel<S, SIDE, DT, 1, false, SLAB>                                   \
-          <<<grid, kThreads, 0, stream>>>(in, out, src_rows, src_cols, rows_b, cols_b);      \
+      direct_transform_kernel<S, SIDE, DT, 1, false, SPAN><<<grid_for(1, SPAN), kThreads, 0,  \
+                                                              stream>>>(in, out, src_rows,   \
+                                                                        src_cols, rows_b,    \
+                                                                        cols_b);             \
   } while (0)
 #define FASTMM_DIRECT(SIDE, DT)                                                              \
   do {                                                                                       \
-    if (slab) FASTMM_DIRECT_LAYOUT(SIDE, DT, true);                                          \
-    else FASTMM_DIRECT_LAYOUT(SIDE, DT, false);                                              \
+    if (span == 64) FASTMM_DIRECT_LAYOUT(SIDE, DT, 64);                                      \
+    else if (span == 32) FASTMM_DIRECT_LAYOUT(SIDE, DT, 32);                                 \
+    else FASTMM_DIRECT_LAYOUT(SIDE, DT, 0);                                                  \
   } while (0)
   if (side == kLeftSide) {
     if (dtype == kBF16) FASTMM_DIRECT(kLeftSide, kBF16);

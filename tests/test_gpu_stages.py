@@ -26,6 +26,7 @@ SHAPES = (
     (257, 263, 269),
     (96, 128, 160),
     (300, 256, 192),
+    (33, 255, 47),  # ragged K with Kb % 32 == 0: K-slab output from the scalar path
 )
 DTYPES = (torch.bfloat16, torch.float16)
 DEVICE = torch.device("cuda", 0)
