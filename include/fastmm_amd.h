@@ -24,10 +24,10 @@
  *   x / input      [rows, inner]            dtype (bf16 or fp16)
  *   weight         [columns, inner]         dtype  (F.linear layout)
  *   right          [inner, columns]         dtype  (mm path)
- *   left_transformed  A'[R, Mb, Kb]         fp16   (operand layout below)
- *   right_transformed B'[R, Nb, Kb]         fp16   (operand layout below; the
+ *   left_transformed  A'[R, Mb, Kb]         fp16 or bf16 (operand layout below)
+ *   right_transformed B'[R, Nb, Kb]         fp16 or bf16 (operand layout below; the
  *        reference stores [R, Kb, Nb] and transposes inside torch.bmm)
- *   products       P[R, Mb, Nb]             fp16 or fp32, row-major
+ *   products       P[R, Mb, Nb]             fp16, bf16 or fp32, row-major
  *   bias           [columns]                dtype
  *   output         [rows, columns]          dtype
  *
@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define FASTMM_ABI_VERSION 2
+#define FASTMM_ABI_VERSION 3
 
 #define FASTMM_OK 0
 #define FASTMM_ERROR_ARGUMENT 1    /* bad pointer, size, dtype or scheme */
@@ -74,35 +74,39 @@ const char* fastmm_last_error(void);
 int fastmm_scheme_info(int scheme, int* size, int* rank);
 const char* fastmm_scheme_sha256(int scheme);
 
-/* A-side transform x[rows, inner] -> A'[R, Mb, Kb] fp16.
- * Replaces _LinearPlan._transform_left + left_transform_kernel
- * (runtime.py:597-615; generated/rank7_2x2x2.py:9-62). */
-int fastmm_left_transform(int scheme, int dtype, const void* input, void* left_transformed,
-                          int64_t rows, int64_t inner, void* stream);
+/* A-side transform x[rows, inner] (dtype) -> A'[R, Mb, Kb] in plane_dtype
+ * (FASTMM_FP16 or FASTMM_BF16: the plan's compute dtype, fp32 program value
+ * rounded to nearest even). Replaces _LinearPlan._transform_left +
+ * left_transform_kernel (runtime.py:597-615; generated/rank7_2x2x2.py:9-62),
+ * whose planes have the plan's compute dtype (runtime.py:216-252). */
+int fastmm_left_transform(int scheme, int dtype, int plane_dtype, const void* input,
+                          void* left_transformed, int64_t rows, int64_t inner, void* stream);
 
-/* Weight transform W[columns, inner] -> B'[R, Nb, Kb] fp16 (prepack and the
- * dynamic path). Replaces _LinearPlan._transform_weight +
+/* Weight transform W[columns, inner] -> B'[R, Nb, Kb] in plane_dtype (prepack
+ * and the dynamic path). Replaces _LinearPlan._transform_weight +
  * right_transform_weight_kernel (runtime.py:637-655; rank7_2x2x2.py:121-204). */
-int fastmm_weight_transform(int scheme, int dtype, const void* weight, void* right_transformed,
-                            int64_t columns, int64_t inner, void* stream);
+int fastmm_weight_transform(int scheme, int dtype, int plane_dtype, const void* weight,
+                            void* right_transformed, int64_t columns, int64_t inner, void* stream);
 
-/* Right transform right[inner, columns] -> B'[R, Nb, Kb] fp16 (mm path).
- * Replaces _LinearPlan._transform_right + right_transform_kernel
+/* Right transform right[inner, columns] -> B'[R, Nb, Kb] in plane_dtype (mm
+ * path). Replaces _LinearPlan._transform_right + right_transform_kernel
  * (runtime.py:617-635; rank7_2x2x2.py:65-118). */
-int fastmm_right_transform(int scheme, int dtype, const void* right, void* right_transformed,
-                           int64_t inner, int64_t columns, void* stream);
+int fastmm_right_transform(int scheme, int dtype, int plane_dtype, const void* right,
+                           void* right_transformed, int64_t inner, int64_t columns, void* stream);
 
-/* Leaf products P[r] = A'[r] @ B'[r]^T for r < rank, fp32 accumulation on
- * FP16 MFMA, stored as products_dtype (FASTMM_FP16 = the reference's
- * rounding, FASTMM_FP32 = no product rounding).
+/* Leaf products P[r] = A'[r] @ B'[r]^T for r < rank on FP16 or BF16 MFMA
+ * (operand_dtype = the planes' type) with fp32 accumulation, stored as
+ * products_dtype: operand_dtype (the reference's torch.bmm rounding) or
+ * FASTMM_FP32 (no product rounding).
  * Replaces torch.bmm(A', B', out=P) (runtime.py:728-732, 768-772). */
-int fastmm_leaf_products(int rank, const void* left_transformed, const void* right_transformed,
-                         void* products, int products_dtype, int64_t block_rows,
-                         int64_t block_inner, int64_t block_columns, void* stream);
+int fastmm_leaf_products(int rank, int operand_dtype, const void* left_transformed,
+                         const void* right_transformed, void* products, int products_dtype,
+                         int64_t block_rows, int64_t block_inner, int64_t block_columns,
+                         void* stream);
 
-/* Output recombination P[R, Mb, Nb] -> output[rows, columns] in dtype, with
- * an optional bias[columns] (NULL = none) added in fp32 after the scheme's
- * sum. Replaces _reconstruct / _reconstruct_bias + output_transform[_bias]_kernel
+/* Output recombination P[R, Mb, Nb] (products_dtype: fp16, bf16 or fp32) ->
+ * output[rows, columns] in dtype, with an optional bias[columns] (NULL = none)
+ * added in fp32 after the scheme's sum. Replaces _reconstruct / _reconstruct_bias + output_transform[_bias]_kernel
  * (runtime.py:657-698; rank7_2x2x2.py:207-345). */
 int fastmm_reconstruct(int scheme, int products_dtype, const void* products, const void* bias,
                        int dtype, void* output, int64_t rows, int64_t columns, void* stream);

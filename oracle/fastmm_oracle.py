@@ -10,14 +10,18 @@ It restates, in numpy, the stage order and rounding points of the reference
 
 * block partition ``Mb = ceil(M/s)`` etc.: ``src/rdna3_fastmm/runtime.py:66-78``;
 * A-side transform: every input block loaded as fp32 (zero past ``M``/``K``),
-  the left program evaluated in fp32, every output plane stored as fp16
-  (round to nearest even): ``generated/rank7_2x2x2.py:9-62`` and the emitter
+  the left program evaluated in fp32, every output plane stored in the plan's
+  compute dtype, fp16 or bf16 (round to nearest even; the planes are
+  allocated with ``compute_dtype``, ``runtime.py:233-250``, and ``tl.store``
+  casts into them, ``generated/rank49_4x4x4.py:31-33``):
+  ``generated/rank7_2x2x2.py:9-62`` and the emitter
   ``tools/generate_triton_scheme.py:133-233``;
 * weight transform from row-major ``W[N, K]`` (block ``j`` of ``W^T``):
   ``generated/rank7_2x2x2.py:121-204``, emitter ``generate_triton_scheme.py:
   240-337``;
-* leaf products ``P[r] = A'[r] @ B'[r]`` with fp16 operands: ``runtime.py:
-  728-732, 768-772`` (``torch.bmm``; fp32 accumulation, fp16 result);
+* leaf products ``P[r] = A'[r] @ B'[r]`` with fp16 or bf16 operands:
+  ``runtime.py:728-732, 768-772`` (``torch.bmm``; fp32 accumulation, result
+  in the operands' type);
 * reconstruction in fp32, ``+ bias`` after the whole expression, stored as
   the output dtype: ``generated/rank7_2x2x2.py:207-345``, emitter
   ``generate_triton_scheme.py:190-232``; output numbering column-major for
@@ -259,39 +263,55 @@ def _blocks(source: np.ndarray, s: int, rows_b: int, cols_b: int, transpose: boo
     return blocks
 
 
-def left_transform(scheme: OracleScheme, x: np.ndarray) -> np.ndarray:
-    """x[M, K] (values exact in fp32) -> A'[R, Mb, Kb] fp16."""
+def _store_planes(planes: list, plane_dtype: str) -> np.ndarray:
+    """fp32 program values -> planes in the plan's compute dtype.
+
+    ``"fp16"``: an ``np.float16`` array. ``"bf16"``: an ``np.float32`` array
+    holding the bf16-rounded values (numpy has no bf16; ``round_to_bf16`` of
+    it gives the bits exactly).
+    """
+    values = np.stack([np.asarray(p, dtype=np.float32) for p in planes])
+    if plane_dtype == "bf16":
+        return bf16_bits_to_f32(round_to_bf16(values)).reshape(values.shape)
+    return values.astype(np.float16)
+
+
+def left_transform(scheme: OracleScheme, x: np.ndarray, plane_dtype: str = "fp16") -> np.ndarray:
+    """x[M, K] (values exact in fp32) -> A'[R, Mb, Kb] in plane_dtype."""
     M, K = x.shape
     s = scheme.size
     planes = evaluate_program(scheme.left, _blocks(x, s, ceil_div(M, s), ceil_div(K, s), False))
-    return np.stack([np.asarray(p, dtype=np.float32) for p in planes]).astype(np.float16)
+    return _store_planes(planes, plane_dtype)
 
 
-def weight_transform(scheme: OracleScheme, weight: np.ndarray) -> np.ndarray:
-    """W[N, K] -> B'[R, Nb, Kb] fp16 (plane r is (sum_j V[r,j] W^T_j)^T)."""
+def weight_transform(scheme: OracleScheme, weight: np.ndarray, plane_dtype: str = "fp16") -> np.ndarray:
+    """W[N, K] -> B'[R, Nb, Kb] in plane_dtype (plane r is (sum_j V[r,j] W^T_j)^T)."""
     N, K = weight.shape
     s = scheme.size
     planes = evaluate_program(scheme.right, _blocks(weight, s, ceil_div(N, s), ceil_div(K, s), True))
-    return np.stack([np.asarray(p, dtype=np.float32) for p in planes]).astype(np.float16)
+    return _store_planes(planes, plane_dtype)
 
 
-def right_transform(scheme: OracleScheme, right: np.ndarray) -> np.ndarray:
-    """right[K, N] (the mm path) -> B'[R, Nb, Kb] fp16, same planes as the weight path."""
-    return weight_transform(scheme, np.ascontiguousarray(right.T))
+def right_transform(scheme: OracleScheme, right: np.ndarray, plane_dtype: str = "fp16") -> np.ndarray:
+    """right[K, N] (the mm path) -> B'[R, Nb, Kb], same planes as the weight path."""
+    return weight_transform(scheme, np.ascontiguousarray(right.T), plane_dtype)
 
 
 def leaf_products(a: np.ndarray, b: np.ndarray, product_dtype: str = "fp16", accumulate: str = "f64") -> np.ndarray:
-    """P[r] = A'[r] @ B'[r]^T from fp16 planes.
+    """P[r] = A'[r] @ B'[r]^T from fp16 or bf16 planes (as returned above).
 
     ``accumulate="f64"`` is the near-exact sum (the parity reference; every
-    fp16 x fp16 product is exact in fp32 and the fp64 sum rounds once);
-    ``"f32"`` is an fp32 BLAS sum (the CPU baseline). ``product_dtype`` is
-    ``"fp16"`` (the reference's ``torch.bmm`` output) or ``"fp32"``.
+    fp16 x fp16 or bf16 x bf16 product is exact in fp32 and the fp64 sum
+    rounds once); ``"f32"`` is an fp32 BLAS sum (the CPU baseline).
+    ``product_dtype`` is ``"fp16"`` or ``"bf16"`` (the reference's
+    ``torch.bmm`` output in the operands' type, via fp32) or ``"fp32"``.
     """
     work = np.float64 if accumulate == "f64" else np.float32
     products = np.matmul(a.astype(work), np.swapaxes(b.astype(work), 1, 2))
     if product_dtype == "fp16":
         return products.astype(np.float16)
+    if product_dtype == "bf16":
+        return bf16_bits_to_f32(round_to_bf16(products.astype(np.float32))).reshape(products.shape)
     return products.astype(np.float32)
 
 
@@ -339,10 +359,11 @@ def linear(
     product_dtype: str = "fp16",
     accumulate: str = "f64",
     out_dtype: str = "bf16",
+    plane_dtype: str = "fp16",
 ) -> np.ndarray:
     """F.linear(x, W, bias) through the scheme, reference stage order."""
-    a = left_transform(scheme, x)
-    b = weight_transform(scheme, weight)
+    a = left_transform(scheme, x, plane_dtype)
+    b = weight_transform(scheme, weight, plane_dtype)
     p = leaf_products(a, b, product_dtype, accumulate)
     return reconstruct(scheme, p, x.shape[0], weight.shape[0], bias, out_dtype)
 
@@ -354,10 +375,11 @@ def matmul(
     product_dtype: str = "fp16",
     accumulate: str = "f64",
     out_dtype: str = "fp16",
+    plane_dtype: str = "fp16",
 ) -> np.ndarray:
     """left[M, K] @ right[K, N] through the scheme (the plan ``run`` path)."""
-    a = left_transform(scheme, left)
-    b = right_transform(scheme, right)
+    a = left_transform(scheme, left, plane_dtype)
+    b = right_transform(scheme, right, plane_dtype)
     p = leaf_products(a, b, product_dtype, accumulate)
     return reconstruct(scheme, p, left.shape[0], right.shape[1], None, out_dtype)
 

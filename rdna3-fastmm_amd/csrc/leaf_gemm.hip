@@ -71,6 +71,20 @@ __device__ __forceinline__ void decode_tile(int wg, int total, int tiles_m, int 
   tn = within / rows_in_group;
 }
 
+// 32x32x16 MFMA on 8 operand elements per lane, fp16 or bf16 (same register
+// bits, different instruction).
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+template <int kIn>
+__device__ __forceinline__ float16v mfma_32x32x16(half8 a, half8 b, float16v c) {
+  if constexpr (kIn == kBF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+}
+
 // ----------------------------------------------------------------- fast path
 
 namespace fast {
@@ -97,7 +111,7 @@ __device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory
 typedef const void __attribute__((address_space(1)))* global_ptr;
 typedef void __attribute__((address_space(3)))* lds_ptr;
 
-template <int kOut>
+template <int kIn, int kOut>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B,
                       void* __restrict__ P, int Mb, int Nb, int Kb, int tiles_m, int tiles_n,
@@ -177,7 +191,7 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[slot][j], fa[slot][i], acc[i][j], 0, 0, 0);
+        acc[i][j] = mfma_32x32x16<kIn>(fb[slot][j], fa[slot][i], acc[i][j]);
   };
   // The 8 fragment reads go under the first 8 MFMAs (they are needed one
   // k-step later); the refill loads, when present, under the second half.
@@ -251,7 +265,7 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
         }
     }
   } else {
-    // Stage the 256 x 256 fp16 tile in LDS, then store 16-byte row segments.
+    // Stage the 256 x 256 16-bit tile in LDS, then store 16-byte row segments.
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     uint16_t* staged = reinterpret_cast<uint16_t*>(smem);
 #pragma unroll
@@ -264,7 +278,7 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
           const int col = wn * 128 + j * 32 + 8 * g + 4 * lane_half;
           uint16_t h[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) h[e] = f32_to_fp16(acc[i][j][4 * g + e]);
+          for (int e = 0; e < 4; ++e) h[e] = from_f32<kOut>(acc[i][j][4 * g + e]);
           store16<4>(staged + row * OUT_PITCH + col, h);
         }
     }
@@ -335,7 +349,7 @@ using Int = std::integral_constant<int, V>;
 template <bool V>
 using Bool = std::integral_constant<bool, V>;
 
-template <int kOut>
+template <int kIn, int kOut>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B,
                       void* __restrict__ P, int Mb, int Nb, int Kb, int tiles_m, int tiles_n,
@@ -416,9 +430,16 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
                      "i"((((kSlotSrc) % 2) * STAGE_HALVES + ((r) - 8) * 16 * BK) * 2));             \
   } while (0)
 #define FASTMM_MFMA(kSet, q)                                                                        \
-  asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0"                                             \
-               : "+a"(acc[(q) / 8][(q) % 8])                                                        \
-               : "v"(fb[kSet][(q) % 8]), "v"(fa[kSet][(q) / 8]))
+  do {                                                                                              \
+    if constexpr (kIn == kBF16)                                                                     \
+      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"                                        \
+                   : "+a"(acc[(q) / 8][(q) % 8])                                                    \
+                   : "v"(fb[kSet][(q) % 8]), "v"(fa[kSet][(q) / 8]));                               \
+    else                                                                                            \
+      asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0"                                         \
+                   : "+a"(acc[(q) / 8][(q) % 8])                                                    \
+                   : "v"(fb[kSet][(q) % 8]), "v"(fa[kSet][(q) / 8]));                               \
+  } while (0)
   // 4 MFMAs with one fragment read for the next slice; a refill after every other group
 #define FASTMM_GROUP(g)                                                                             \
   do {                                                                                              \
@@ -519,7 +540,7 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
       }
     }
   } else {
-    // Stage the 256 x 256 fp16 tile in LDS (8-byte writes: 32 lanes cover all
+    // Stage the 256 x 256 16-bit tile in LDS (8-byte writes: 32 lanes cover all
     // 64 banks at row pitch 264 halves), then store 16-byte row segments.
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     uint16_t* staged = reinterpret_cast<uint16_t*>(smem);
@@ -531,7 +552,7 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
         const int col = wn * 128 + j * 16 + 4 * fc;
         uint16_t h[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) h[e] = f32_to_fp16(acc[i][j][e]);
+        for (int e = 0; e < 4; ++e) h[e] = from_f32<kOut>(acc[i][j][e]);
         store16<4>(staged + row * fast::OUT_PITCH + col, h);
       }
     }
@@ -569,7 +590,7 @@ __device__ __forceinline__ int swizzled(int row, int chunk) {
 
 // kSlabLayout: operand planes are K-slab-major (Kb % 32 == 0); a thread's 8
 // consecutive k stay inside one slab row.
-template <bool kAligned, int kOut, bool kSlabLayout>
+template <bool kAligned, int kIn, int kOut, bool kSlabLayout>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B,
                       void* __restrict__ P, int Mb, int Nb, int Kb, int tiles_m, int tiles_n,
@@ -651,7 +672,7 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = mfma_32x32x16<kIn>(af[i], bf[j], acc[i][j]);
     }
     if (kt + 1 < k_tiles) lds_store(buffer ^ 1);
     __syncthreads();
@@ -672,7 +693,7 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
         if (row < Mb) {
           const int64_t offset = leaf_offset + static_cast<int64_t>(row) * Nb + col;
           if constexpr (kOut == kFP32) static_cast<float*>(P)[offset] = acc[i][j][e];
-          else static_cast<uint16_t*>(P)[offset] = f32_to_fp16(acc[i][j][e]);
+          else static_cast<uint16_t*>(P)[offset] = from_f32<kOut>(acc[i][j][e]);
         }
       }
     }
@@ -723,7 +744,38 @@ bool mfma16_leaf_gemm_applies(int64_t mb, int64_t kb, int64_t nb) {
 
 using namespace fastmm;
 
-extern "C" int fastmm_leaf_products(int rank, const void* left_transformed,
+namespace fastmm {
+
+// Kernel choice for one (operand, products) element-type pair.
+template <int kIn, int kOut>
+int launch_leaf_products(const void* a, const void* b, void* p, int64_t rank, int64_t mb, int64_t kb,
+                         int64_t nb, hipStream_t s) {
+  if (fast_leaf_gemm_applies(a, b, p, kb, nb, kOut) && mfma16_leaf_gemm_applies(mb, kb, nb)) {
+    return launch_tiles(mfma16::leaf_gemm_kernel<kIn, kOut>, mfma16::LDS_BYTES, a, b, p, rank, mb, kb, nb, s);
+  }
+  if (fast_leaf_gemm_applies(a, b, p, kb, nb, kOut)) {
+    return launch_tiles(fast::leaf_gemm_kernel<kIn, kOut>, fast::LDS_BYTES, a, b, p, rank, mb, kb, nb, s);
+  }
+  const bool aligned = kb % 8 == 0 && aligned_to(a, 16) && aligned_to(b, 16);
+  if (slab_layout(kb)) {
+    if (aligned) {
+      return launch_tiles(generic::leaf_gemm_kernel<true, kIn, kOut, true>, generic::LDS_BYTES, a, b, p, rank,
+                          mb, kb, nb, s);
+    }
+    return launch_tiles(generic::leaf_gemm_kernel<false, kIn, kOut, true>, generic::LDS_BYTES, a, b, p, rank,
+                        mb, kb, nb, s);
+  }
+  if (aligned) {
+    return launch_tiles(generic::leaf_gemm_kernel<true, kIn, kOut, false>, generic::LDS_BYTES, a, b, p, rank,
+                        mb, kb, nb, s);
+  }
+  return launch_tiles(generic::leaf_gemm_kernel<false, kIn, kOut, false>, generic::LDS_BYTES, a, b, p, rank,
+                      mb, kb, nb, s);
+}
+
+}  // namespace fastmm
+
+extern "C" int fastmm_leaf_products(int rank, int operand_dtype, const void* left_transformed,
                                     const void* right_transformed, void* products,
                                     int products_dtype, int64_t block_rows, int64_t block_inner,
                                     int64_t block_columns, void* stream) {
@@ -734,8 +786,13 @@ extern "C" int fastmm_leaf_products(int rank, const void* left_transformed,
   if (rank < 1 || block_rows < 1 || block_inner < 1 || block_columns < 1) {
     return fail(FASTMM_ERROR_ARGUMENT, "leaf products: dimensions must be positive");
   }
-  if (products_dtype != kFP16 && products_dtype != kFP32) {
-    return fail(FASTMM_ERROR_ARGUMENT, "leaf products: products must be fp16 or fp32");
+  if (operand_dtype != kFP16 && operand_dtype != kBF16) {
+    return fail(FASTMM_ERROR_ARGUMENT, "leaf products: operands must be fp16 or bf16");
+  }
+  if (products_dtype != operand_dtype && products_dtype != kFP32) {
+    return fail(FASTMM_ERROR_ARGUMENT,
+                "leaf products: products must be fp32 or the operands' type (%d), got %d",
+                operand_dtype, products_dtype);
   }
   if (block_rows * block_inner > INT32_MAX || block_columns * block_inner > INT32_MAX ||
       block_rows * block_columns > INT32_MAX) {
@@ -746,33 +803,10 @@ extern "C" int fastmm_leaf_products(int rank, const void* left_transformed,
   const void* b = right_transformed;
   void* p = products;
   const int64_t mb = block_rows, kb = block_inner, nb = block_columns;
-  if (fast_leaf_gemm_applies(a, b, p, kb, nb, products_dtype) && mfma16_leaf_gemm_applies(mb, kb, nb)) {
-    if (products_dtype == kFP32) {
-      return launch_tiles(mfma16::leaf_gemm_kernel<kFP32>, mfma16::LDS_BYTES, a, b, p, rank, mb, kb, nb, s);
-    }
-    return launch_tiles(mfma16::leaf_gemm_kernel<kFP16>, mfma16::LDS_BYTES, a, b, p, rank, mb, kb, nb, s);
+  if (operand_dtype == kBF16) {
+    if (products_dtype == kFP32) return launch_leaf_products<kBF16, kFP32>(a, b, p, rank, mb, kb, nb, s);
+    return launch_leaf_products<kBF16, kBF16>(a, b, p, rank, mb, kb, nb, s);
   }
-  if (fast_leaf_gemm_applies(a, b, p, kb, nb, products_dtype)) {
-    if (products_dtype == kFP32) {
-      return launch_tiles(fast::leaf_gemm_kernel<kFP32>, fast::LDS_BYTES, a, b, p, rank, mb, kb, nb, s);
-    }
-    return launch_tiles(fast::leaf_gemm_kernel<kFP16>, fast::LDS_BYTES, a, b, p, rank, mb, kb, nb, s);
-  }
-  const bool aligned = kb % 8 == 0 && aligned_to(a, 16) && aligned_to(b, 16);
-#define FASTMM_GENERIC(ALIGNED, SLAB)                                                                       \
-  do {                                                                                                      \
-    if (products_dtype == kFP32) {                                                                          \
-      return launch_tiles(generic::leaf_gemm_kernel<ALIGNED, kFP32, SLAB>, generic::LDS_BYTES, a, b, p,     \
-                          rank, mb, kb, nb, s);                                                             \
-    }                                                                                                       \
-    return launch_tiles(generic::leaf_gemm_kernel<ALIGNED, kFP16, SLAB>, generic::LDS_BYTES, a, b, p, rank, \
-                        mb, kb, nb, s);                                                                     \
-  } while (0)
-  if (slab_layout(kb)) {
-    if (aligned) FASTMM_GENERIC(true, true);
-    FASTMM_GENERIC(false, true);
-  }
-  if (aligned) FASTMM_GENERIC(true, false);
-  FASTMM_GENERIC(false, false);
-#undef FASTMM_GENERIC
+  if (products_dtype == kFP32) return launch_leaf_products<kFP16, kFP32>(a, b, p, rank, mb, kb, nb, s);
+  return launch_leaf_products<kFP16, kFP16>(a, b, p, rank, mb, kb, nb, s);
 }

@@ -33,6 +33,8 @@ enum Side : int { kLeftSide = 0, kWeightSide = 1 };
 // Left:   input j = x block (j / s, j % s)      over x[src_rows, src_cols].
 // Weight: input j = W^T block (j / s, j % s) = W block (j % s, j / s) over
 //         W[src_rows = N, src_cols = K]; plane r of B' is [Nb, Kb].
+// kPlane: element type of the transformed planes (kFP16 or kBF16, round to
+// nearest even from the fp32 program value).
 // kVector: src_cols == s * cols_b, cols_b % EPT == 0 and 2*EPT-aligned
 // pointers, so every vector is wholly inside a row; otherwise EPT == 1.
 // kSpan == 0: row-major output planes; a 1D grid walks them in storage order.
@@ -40,7 +42,7 @@ enum Side : int { kLeftSide = 0, kWeightSide = 1 };
 // grid gives each wave RPW rows x kSpan columns, so a wave reads whole 64- or
 // 128-byte line runs of every input row and writes RPW consecutive slab rows
 // (RPW * 64 bytes) per slab and plane.
-template <class S, int kSide, int kDType, int EPT, bool kVector, int kSpan>
+template <class S, int kSide, int kDType, int kPlane, int EPT, bool kVector, int kSpan>
 __global__ __launch_bounds__(kThreads) void direct_transform_kernel(
     const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, int64_t src_rows,
     int64_t src_cols, int64_t rows_b, int64_t cols_b) {
@@ -80,7 +82,7 @@ __global__ __launch_bounds__(kThreads) void direct_transform_kernel(
     }
   };
   auto store = [&](int k, const Vec<EPT>& v) {
-    store_vec<kFP16, EPT>(dst + k * plane + at, v);
+    store_vec<kPlane, EPT>(dst + k * plane + at, v);
   };
   if constexpr (kSide == kLeftSide) {
     S::template left<Vec<EPT>>(load, store);
@@ -96,7 +98,7 @@ __global__ __launch_bounds__(kThreads) void direct_transform_kernel(
 constexpr int kTransposeTile = 32;
 static_assert(kTransposeTile == kSlab, "a transpose tile covers exactly one K slab");
 
-template <class S, int kDType, bool kSlabLayout>
+template <class S, int kDType, int kPlane, bool kSlabLayout>
 __global__ __launch_bounds__(kThreads) void transposed_right_kernel(
     const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, int64_t inner,
     int64_t columns, int64_t kb, int64_t nb) {
@@ -138,7 +140,7 @@ __global__ __launch_bounds__(kThreads) void transposed_right_kernel(
     uint16_t* p = dst + static_cast<int64_t>(r) * nb * kb + operand_offset<kSlabLayout>(n, k, nb, kb);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      if (k + e < kb) p[e] = f32_to_fp16(v.v[e]);
+      if (k + e < kb) p[e] = from_f32<kPlane>(v.v[e]);
     }
   };
   S::template right<Vec<4>>(load, store);
@@ -167,7 +169,7 @@ __device__ __forceinline__ Vec<EPT> load_product(const void* products, int64_t o
     }
     return v;
   } else {
-    return load_vec<kFP16, EPT>(static_cast<const uint16_t*>(products) + offset);
+    return load_vec<kProd, EPT>(static_cast<const uint16_t*>(products) + offset);
   }
 }
 
@@ -213,7 +215,7 @@ __global__ __launch_bounds__(kThreads) void reconstruct_kernel(
 // ------------------------------------------------------------- launchers
 
 template <class S>
-int launch_direct(int side, int dtype, const void* src, void* dst, int64_t src_rows,
+int launch_direct(int side, int dtype, int plane_dtype, const void* src, void* dst, int64_t src_rows,
                   int64_t src_cols, hipStream_t stream) {
   constexpr int s = S::kSize;
   constexpr int W = vector_width<S>();
@@ -233,24 +235,30 @@ int launch_direct(int side, int dtype, const void* src, void* dst, int64_t src_r
     const int64_t rows_per_block = static_cast<int64_t>(kThreads / 64) * (64 / (kspan / ept));
     return dim3(static_cast<unsigned>(ceil_div(rows_b, rows_per_block)), static_cast<unsigned>(cols_b / kspan));
   };
-#define FASTMM_DIRECT_LAYOUT(SIDE, DT, SPAN)                                                 \
-  do {                                                                                       \
-    if (vector)                                                                              \
-      direct_transform_kernel<S, SIDE, DT, W, true, SPAN><<<grid_for(W, SPAN), kThreads, 0,   \
-                                                             stream>>>(in, out, src_rows,    \
-                                                                       src_cols, rows_b,     \
-                                                                       cols_b);              \
-    else                                                                                     \
-      direct_transform_kernel<S, SIDE, DT, 1, false, SPAN><<<grid_for(1, SPAN), kThreads, 0,  \
-                                                              stream>>>(in, out, src_rows,   \
-                                                                        src_cols, rows_b,    \
-                                                                        cols_b);             \
+#define FASTMM_DIRECT_LAYOUT(SIDE, DT, PL, SPAN)                                              \
+  do {                                                                                        \
+    if (vector)                                                                               \
+      direct_transform_kernel<S, SIDE, DT, PL, W, true, SPAN><<<grid_for(W, SPAN), kThreads, 0, \
+                                                                 stream>>>(in, out, src_rows,  \
+                                                                           src_cols, rows_b,   \
+                                                                           cols_b);            \
+    else                                                                                      \
+      direct_transform_kernel<S, SIDE, DT, PL, 1, false, SPAN><<<grid_for(1, SPAN), kThreads,   \
+                                                                  0, stream>>>(in, out,        \
+                                                                               src_rows,       \
+                                                                               src_cols,       \
+                                                                               rows_b, cols_b); \
   } while (0)
-#define FASTMM_DIRECT(SIDE, DT)                                                              \
-  do {                                                                                       \
-    if (span == 64) FASTMM_DIRECT_LAYOUT(SIDE, DT, 64);                                      \
-    else if (span == 32) FASTMM_DIRECT_LAYOUT(SIDE, DT, 32);                                 \
-    else FASTMM_DIRECT_LAYOUT(SIDE, DT, 0);                                                  \
+#define FASTMM_DIRECT_PLANE(SIDE, DT, PL)                                                     \
+  do {                                                                                        \
+    if (span == 64) FASTMM_DIRECT_LAYOUT(SIDE, DT, PL, 64);                                   \
+    else if (span == 32) FASTMM_DIRECT_LAYOUT(SIDE, DT, PL, 32);                              \
+    else FASTMM_DIRECT_LAYOUT(SIDE, DT, PL, 0);                                               \
+  } while (0)
+#define FASTMM_DIRECT(SIDE, DT)                                                               \
+  do {                                                                                        \
+    if (plane_dtype == kBF16) FASTMM_DIRECT_PLANE(SIDE, DT, kBF16);                           \
+    else FASTMM_DIRECT_PLANE(SIDE, DT, kFP16);                                                \
   } while (0)
   if (side == kLeftSide) {
     if (dtype == kBF16) FASTMM_DIRECT(kLeftSide, kBF16);
@@ -260,13 +268,14 @@ int launch_direct(int side, int dtype, const void* src, void* dst, int64_t src_r
     else FASTMM_DIRECT(kWeightSide, kFP16);
   }
 #undef FASTMM_DIRECT
+#undef FASTMM_DIRECT_PLANE
 #undef FASTMM_DIRECT_LAYOUT
   return check_launch(side == kLeftSide ? "left transform" : "weight transform");
 }
 
 template <class S>
-int launch_transposed(int dtype, const void* src, void* dst, int64_t inner, int64_t columns,
-                      hipStream_t stream) {
+int launch_transposed(int dtype, int plane_dtype, const void* src, void* dst, int64_t inner,
+                      int64_t columns, hipStream_t stream) {
   constexpr int s = S::kSize;
   const int64_t kb = ceil_div(inner, s);
   const int64_t nb = ceil_div(columns, s);
@@ -275,13 +284,21 @@ int launch_transposed(int dtype, const void* src, void* dst, int64_t inner, int6
   const uint16_t* in = static_cast<const uint16_t*>(src);
   uint16_t* out = static_cast<uint16_t*>(dst);
   const bool slab = slab_layout(kb);
+#define FASTMM_TRANSPOSED(DT, PL)                                                                       \
+  do {                                                                                                  \
+    if (slab) transposed_right_kernel<S, DT, PL, true><<<grid, kThreads, 0, stream>>>(in, out, inner,   \
+                                                                                       columns, kb, nb); \
+    else transposed_right_kernel<S, DT, PL, false><<<grid, kThreads, 0, stream>>>(in, out, inner,       \
+                                                                                   columns, kb, nb);     \
+  } while (0)
   if (dtype == kBF16) {
-    if (slab) transposed_right_kernel<S, kBF16, true><<<grid, kThreads, 0, stream>>>(in, out, inner, columns, kb, nb);
-    else transposed_right_kernel<S, kBF16, false><<<grid, kThreads, 0, stream>>>(in, out, inner, columns, kb, nb);
+    if (plane_dtype == kBF16) FASTMM_TRANSPOSED(kBF16, kBF16);
+    else FASTMM_TRANSPOSED(kBF16, kFP16);
   } else {
-    if (slab) transposed_right_kernel<S, kFP16, true><<<grid, kThreads, 0, stream>>>(in, out, inner, columns, kb, nb);
-    else transposed_right_kernel<S, kFP16, false><<<grid, kThreads, 0, stream>>>(in, out, inner, columns, kb, nb);
+    if (plane_dtype == kBF16) FASTMM_TRANSPOSED(kFP16, kBF16);
+    else FASTMM_TRANSPOSED(kFP16, kFP16);
   }
+#undef FASTMM_TRANSPOSED
   return check_launch("right transform");
 }
 
@@ -326,6 +343,9 @@ int launch_reconstruct(int products_dtype, const void* products, const void* bia
   if (products_dtype == kFP32) {
     if (dtype == kBF16) FASTMM_RECON(kFP32, kBF16);
     else FASTMM_RECON(kFP32, kFP16);
+  } else if (products_dtype == kBF16) {
+    if (dtype == kBF16) FASTMM_RECON(kBF16, kBF16);
+    else FASTMM_RECON(kBF16, kFP16);
   } else {
     if (dtype == kBF16) FASTMM_RECON(kFP16, kBF16);
     else FASTMM_RECON(kFP16, kFP16);
@@ -343,6 +363,13 @@ int with_scheme(int scheme, F&& f) {
     case FASTMM_SCHEME_RANK49: return f.template operator()<SchemeRank49>();
     default: return fail(FASTMM_ERROR_ARGUMENT, "unknown scheme id %d", scheme);
   }
+}
+
+int check_plane_dtype(const char* name, int plane_dtype) {
+  if (plane_dtype != kFP16 && plane_dtype != kBF16) {
+    return fail(FASTMM_ERROR_ARGUMENT, "%s: planes must be fp16 or bf16, got %d", name, plane_dtype);
+  }
+  return FASTMM_OK;
 }
 
 int check_io(const char* name, int dtype, const void* a, const void* b, int64_t rows,
@@ -382,20 +409,21 @@ extern "C" const char* fastmm_scheme_sha256(int scheme) {
   }
 }
 
-extern "C" int fastmm_left_transform(int scheme, int dtype, const void* input,
+extern "C" int fastmm_left_transform(int scheme, int dtype, int plane_dtype, const void* input,
                                      void* left_transformed, int64_t rows, int64_t inner,
                                      void* stream) {
   clear_error();
   if (int status = check_io("left transform", dtype, input, left_transformed, rows, inner)) {
     return status;
   }
+  if (int status = check_plane_dtype("left transform", plane_dtype)) return status;
   return with_scheme(scheme, [&]<class S>() {
-    return launch_direct<S>(kLeftSide, dtype, input, left_transformed, rows, inner,
+    return launch_direct<S>(kLeftSide, dtype, plane_dtype, input, left_transformed, rows, inner,
                             static_cast<hipStream_t>(stream));
   });
 }
 
-extern "C" int fastmm_weight_transform(int scheme, int dtype, const void* weight,
+extern "C" int fastmm_weight_transform(int scheme, int dtype, int plane_dtype, const void* weight,
                                        void* right_transformed, int64_t columns, int64_t inner,
                                        void* stream) {
   clear_error();
@@ -403,21 +431,23 @@ extern "C" int fastmm_weight_transform(int scheme, int dtype, const void* weight
           check_io("weight transform", dtype, weight, right_transformed, columns, inner)) {
     return status;
   }
+  if (int status = check_plane_dtype("weight transform", plane_dtype)) return status;
   return with_scheme(scheme, [&]<class S>() {
-    return launch_direct<S>(kWeightSide, dtype, weight, right_transformed, columns, inner,
-                            static_cast<hipStream_t>(stream));
+    return launch_direct<S>(kWeightSide, dtype, plane_dtype, weight, right_transformed, columns,
+                            inner, static_cast<hipStream_t>(stream));
   });
 }
 
-extern "C" int fastmm_right_transform(int scheme, int dtype, const void* right,
+extern "C" int fastmm_right_transform(int scheme, int dtype, int plane_dtype, const void* right,
                                       void* right_transformed, int64_t inner, int64_t columns,
                                       void* stream) {
   clear_error();
   if (int status = check_io("right transform", dtype, right, right_transformed, inner, columns)) {
     return status;
   }
+  if (int status = check_plane_dtype("right transform", plane_dtype)) return status;
   return with_scheme(scheme, [&]<class S>() {
-    return launch_transposed<S>(dtype, right, right_transformed, inner, columns,
+    return launch_transposed<S>(dtype, plane_dtype, right, right_transformed, inner, columns,
                                 static_cast<hipStream_t>(stream));
   });
 }
@@ -429,8 +459,8 @@ extern "C" int fastmm_reconstruct(int scheme, int products_dtype, const void* pr
   if (int status = check_io("reconstruct", dtype, products, output, rows, columns)) {
     return status;
   }
-  if (products_dtype != kFP16 && products_dtype != kFP32) {
-    return fail(FASTMM_ERROR_ARGUMENT, "reconstruct: products must be fp16 or fp32");
+  if (products_dtype != kFP16 && products_dtype != kBF16 && products_dtype != kFP32) {
+    return fail(FASTMM_ERROR_ARGUMENT, "reconstruct: products must be fp16, bf16 or fp32");
   }
   return with_scheme(scheme, [&]<class S>() {
     return launch_reconstruct<S>(products_dtype, products, bias, dtype, output, rows, columns,

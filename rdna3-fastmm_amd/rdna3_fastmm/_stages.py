@@ -1,7 +1,9 @@
 """One function per HIP stage: tensors in, a launch on the current stream out.
 
 Shared by the plans (``runtime``) and the allocating operators (``linear``).
-Callers validate shapes, dtypes and storage; these only marshal pointers.
+Callers validate shapes, dtypes and storage; these only marshal pointers. The
+element types passed to the library are the tensors' own: transformed planes
+and leaf operands in the plan's compute dtype, products likewise (or fp32).
 """
 
 from __future__ import annotations
@@ -18,6 +20,7 @@ def left_transform(scheme: Scheme, source: torch.Tensor, output: torch.Tensor, r
             "fastmm_left_transform",
             scheme.scheme_id,
             _native.dtype_code(source.dtype),
+            _native.dtype_code(output.dtype),
             source.data_ptr(),
             output.data_ptr(),
             rows,
@@ -32,6 +35,7 @@ def weight_transform(scheme: Scheme, weight: torch.Tensor, output: torch.Tensor,
             "fastmm_weight_transform",
             scheme.scheme_id,
             _native.dtype_code(weight.dtype),
+            _native.dtype_code(output.dtype),
             weight.data_ptr(),
             output.data_ptr(),
             columns,
@@ -46,6 +50,7 @@ def right_transform(scheme: Scheme, right: torch.Tensor, output: torch.Tensor, i
             "fastmm_right_transform",
             scheme.scheme_id,
             _native.dtype_code(right.dtype),
+            _native.dtype_code(output.dtype),
             right.data_ptr(),
             output.data_ptr(),
             inner,
@@ -67,6 +72,7 @@ def leaf_products(
         _native.call(
             "fastmm_leaf_products",
             rank,
+            _native.dtype_code(left.dtype),
             left.data_ptr(),
             right.data_ptr(),
             products.data_ptr(),

@@ -23,7 +23,7 @@ from torch.fx import GraphModule, Node
 from torch.fx.passes.fake_tensor_prop import FakeTensorProp
 
 from . import _stages
-from .runtime import Rank7Plan, Rank48Plan, Rank49Plan, _check_library_scheme, _LinearPlan
+from .runtime import Rank7Plan, Rank48Plan, Rank49Plan, _check_library_scheme, _LinearPlan, operand_shape
 from .schemes import load_scheme
 
 LINEAR_TARGETS = frozenset({torch._C._nn.linear, torch.ops.aten.linear.default})
@@ -68,8 +68,8 @@ def _linear(plan_type: type, name: str, input_tensor: torch.Tensor, weight: torc
     s, rank = scheme.size, scheme.rank
     mb, kb, nb = _ceil_div(rows, s), _ceil_div(inner, s), _ceil_div(columns, s)
     device = input_tensor.device
-    left = torch.empty((rank, mb, kb), device=device, dtype=torch.float16)
-    right = torch.empty((rank, nb, kb), device=device, dtype=torch.float16)
+    left = torch.empty(operand_shape(rank, mb, kb), device=device, dtype=torch.float16)
+    right = torch.empty(operand_shape(rank, nb, kb), device=device, dtype=torch.float16)
     _stages.left_transform(scheme, flat, left, rows, inner)
     _stages.weight_transform(scheme, weight, right, columns, inner)
     products = torch.empty((rank, mb, nb), device=device, dtype=torch.float16)

@@ -660,7 +660,15 @@ class Rank49Plan(_LinearPlan):
     scheme_key = "rank49"
     rank = 49
     scheme_size = 4
-    precision_pairs = frozenset({(torch.float16, torch.float16), (torch.bfloat16, torch.float16)})
+    # (bf16, bf16): BF16 planes, BF16 MFMA leaves and BF16 products, as the reference
+    # offers (runtime.py:852-858); far less accurate than the fp16-leaf pairs.
+    precision_pairs = frozenset(
+        {
+            (torch.float16, torch.float16),
+            (torch.bfloat16, torch.bfloat16),
+            (torch.bfloat16, torch.float16),
+        }
+    )
 
 
 PLAN_TYPES: dict[str, type[_LinearPlan]] = {"rank7": Rank7Plan, "rank48": Rank48Plan, "rank49": Rank49Plan}

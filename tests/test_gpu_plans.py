@@ -130,6 +130,44 @@ def test_linear_matches_oracle_and_bounded_error(plan_type, shape) -> None:
     assert plan.packed_weight_bytes == plan.packed_right_bytes
 
 
+@pytest.mark.parametrize("shape", ((5, 6, 7), (257, 263, 269), (200, 512, 544)))
+def test_rank49_bf16_leaves_match_oracle_stage_by_stage(shape) -> None:
+    """The reference's (bf16, bf16) rank-49 pair (runtime.py:852-858): BF16 planes,
+    BF16 MFMA leaves and BF16 products, each stage pinned against the oracle."""
+    print(f"\n[case] rank49 bf16 leaves {shape}", flush=True)
+    g = torch.Generator().manual_seed(41)
+    m, k, n = shape
+    x = torch.randn((m, k), generator=g).to(torch.bfloat16)
+    w = torch.randn((n, k), generator=g).to(torch.bfloat16)
+    bias = torch.randn(n, generator=g).to(torch.bfloat16)
+    xg, wg, bg = x.to(DEVICE), w.to(DEVICE), bias.to(DEVICE)
+    plan = Rank49Plan(*shape, device=DEVICE, dtype=torch.bfloat16, compute_dtype=torch.bfloat16)
+    workspace = plan.allocate_workspace(max_free_memory_fraction=0.1)
+    assert workspace.products.dtype == torch.bfloat16
+    dynamic = plan.run_linear(xg, wg, workspace, bg)
+    torch.cuda.synchronize()
+    oracle = O.load_oracle_scheme("rank49")
+    a = O.left_transform(oracle, x.float().numpy(), "bf16")
+    b = O.weight_transform(oracle, w.float().numpy(), "bf16")
+    rank, mb, kb = a.shape
+    nb = b.shape[1]
+    left_bits = from_operand(workspace.left_transformed.cpu().view(torch.int16).numpy(), rank, mb, kb)
+    right_bits = from_operand(workspace.right_transformed.cpu().view(torch.int16).numpy(), rank, nb, kb)
+    assert np.array_equal(left_bits, O.round_to_bf16(a).view(np.int16))
+    assert np.array_equal(right_bits, O.round_to_bf16(b).view(np.int16))
+    products = workspace.products.float().cpu().numpy().astype(np.float64)
+    exact = O.leaf_products(a, b, product_dtype="fp32").astype(np.float64)
+    magnitude = np.matmul(np.abs(a.astype(np.float64)), np.abs(np.swapaxes(b.astype(np.float64), 1, 2)))
+    bound = kb * 2.0**-24 * magnitude + np.abs(exact) * 2.0**-8 + 2.0**-126
+    assert np.all(np.abs(products - exact) <= bound)
+    recombined = O.reconstruct(oracle, workspace.products.float().cpu().numpy(), m, n, bias.float().numpy(), "bf16")
+    assert np.array_equal(dynamic.cpu().view(torch.int16).numpy(), recombined.view(np.int16))
+    packed = plan.pack_weight(wg, max_free_memory_fraction=0.1)
+    packed_ws = plan.allocate_workspace(max_free_memory_fraction=0.1, prepacked_right=True)
+    assert torch.equal(plan.run_linear_packed(xg, packed, packed_ws, bg), dynamic)
+    assert torch.isfinite(dynamic).all()
+
+
 def test_packed_weight_reuses_across_rows_and_rejects_other_shape() -> None:
     """reference test_rdna3.py:616-677."""
     torch.manual_seed(37)

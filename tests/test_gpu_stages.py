@@ -53,11 +53,18 @@ def _bits(t: torch.Tensor) -> np.ndarray:
     return t.detach().cpu().view(torch.int16).numpy()
 
 
+def _plane_bits(planes: np.ndarray, plane_dtype: str) -> np.ndarray:
+    if plane_dtype == "bf16":
+        return O.round_to_bf16(planes).view(np.int16)
+    return planes.view(np.int16)
+
+
 @pytest.mark.parametrize("key", SCHEME_KEYS)
 @pytest.mark.parametrize("shape", SHAPES)
 @pytest.mark.parametrize("dtype", DTYPES)
-def test_transforms_bit_exact(key, shape, dtype) -> None:
-    print(f"\n[case] transforms {key} {shape} {dtype}", flush=True)
+@pytest.mark.parametrize("plane_dtype", ("fp16", "bf16"))
+def test_transforms_bit_exact(key, shape, dtype, plane_dtype) -> None:
+    print(f"\n[case] transforms {key} {shape} {dtype} -> {plane_dtype} planes", flush=True)
     scheme = load_scheme(key)
     oracle = O.load_oracle_scheme(key)
     m, k, n = shape
@@ -65,16 +72,17 @@ def test_transforms_bit_exact(key, shape, dtype) -> None:
     x, w, _ = _inputs(shape, dtype, seed=m + k + n)
     xg, wg = x.to(DEVICE), w.to(DEVICE)
     mb, kb, nb = _ceil(m, s), _ceil(k, s), _ceil(n, s)
-    a = torch.empty(operand_shape(r, mb, kb), device=DEVICE, dtype=torch.float16)
-    b = torch.empty(operand_shape(r, nb, kb), device=DEVICE, dtype=torch.float16)
+    planes = torch.bfloat16 if plane_dtype == "bf16" else torch.float16
+    a = torch.empty(operand_shape(r, mb, kb), device=DEVICE, dtype=planes)
+    b = torch.empty(operand_shape(r, nb, kb), device=DEVICE, dtype=planes)
     b2 = torch.empty_like(b)
     _stages.left_transform(scheme, xg, a, m, k)
     _stages.weight_transform(scheme, wg, b, n, k)
     right = wg.t().contiguous()
     _stages.right_transform(scheme, right, b2, k, n)
     torch.cuda.synchronize()
-    expect_a = O.left_transform(oracle, _np(x)).view(np.int16)
-    expect_b = O.weight_transform(oracle, _np(w)).view(np.int16)
+    expect_a = _plane_bits(O.left_transform(oracle, _np(x), plane_dtype), plane_dtype)
+    expect_b = _plane_bits(O.weight_transform(oracle, _np(w), plane_dtype), plane_dtype)
     assert np.array_equal(from_operand(_bits(a), r, mb, kb), expect_a)
     assert np.array_equal(from_operand(_bits(b), r, nb, kb), expect_b)
     assert np.array_equal(from_operand(_bits(b2), r, nb, kb), expect_b)
@@ -82,7 +90,7 @@ def test_transforms_bit_exact(key, shape, dtype) -> None:
 
 @pytest.mark.parametrize("key", SCHEME_KEYS)
 @pytest.mark.parametrize("shape", SHAPES)
-@pytest.mark.parametrize("product_dtype", (torch.float16, torch.float32))
+@pytest.mark.parametrize("product_dtype", (torch.float16, torch.bfloat16, torch.float32))
 def test_reconstruct_bit_exact(key, shape, product_dtype) -> None:
     print(f"\n[case] reconstruct {key} {shape} {product_dtype}", flush=True)
     scheme = load_scheme(key)
@@ -99,7 +107,7 @@ def test_reconstruct_bit_exact(key, shape, product_dtype) -> None:
             torch.cuda.synchronize()
             expected = O.reconstruct(
                 oracle,
-                products.float().numpy() if product_dtype == torch.float32 else products.numpy(),
+                products.numpy() if product_dtype == torch.float16 else products.float().numpy(),
                 m,
                 n,
                 _np(bias) if use_bias else None,
@@ -121,23 +129,36 @@ def test_reconstruct_bit_exact(key, shape, product_dtype) -> None:
         (4, 255, 264, 512),
     ),
 )
-@pytest.mark.parametrize("product_dtype", (torch.float16, torch.float32))
-def test_leaf_products_within_fp32_accumulation_bound(dims, product_dtype) -> None:
+@pytest.mark.parametrize(
+    ("operand_dtype", "product_dtype"),
+    (
+        (torch.float16, torch.float16),
+        (torch.float16, torch.float32),
+        (torch.bfloat16, torch.bfloat16),
+        (torch.bfloat16, torch.float32),
+    ),
+)
+def test_leaf_products_within_fp32_accumulation_bound(dims, operand_dtype, product_dtype) -> None:
     rank, mb, nb, kb = dims
-    print(f"\n[case] leaf products {dims} {product_dtype}", flush=True)
+    print(f"\n[case] leaf products {dims} {operand_dtype} -> {product_dtype}", flush=True)
     g = torch.Generator().manual_seed(sum(dims))
-    a = torch.randn((rank, mb, kb), generator=g).half()
-    b = torch.randn((rank, nb, kb), generator=g).half()
+    a = torch.randn((rank, mb, kb), generator=g).to(operand_dtype)
+    b = torch.randn((rank, nb, kb), generator=g).to(operand_dtype)
     p = torch.empty((rank, mb, nb), device=DEVICE, dtype=product_dtype)
-    a_dev = torch.from_numpy(to_operand(a.numpy())).to(DEVICE)
-    b_dev = torch.from_numpy(to_operand(b.numpy())).to(DEVICE)
+    # operand buffers in the kernels' layout (bit patterns moved as int16)
+    a_dev = torch.from_numpy(to_operand(a.view(torch.int16).numpy())).to(DEVICE).view(operand_dtype)
+    b_dev = torch.from_numpy(to_operand(b.view(torch.int16).numpy())).to(DEVICE).view(operand_dtype)
     _stages.leaf_products(rank, a_dev, b_dev, p, mb, kb, nb)
     torch.cuda.synchronize()
-    exact = O.leaf_products(a.numpy(), b.numpy(), product_dtype="fp32")
-    magnitude = np.matmul(np.abs(a.numpy().astype(np.float64)), np.abs(np.swapaxes(b.numpy().astype(np.float64), 1, 2)))
+    a32, b32 = a.float().numpy(), b.float().numpy()
+    exact = O.leaf_products(a32, b32, product_dtype="fp32")
+    magnitude = np.matmul(np.abs(a32.astype(np.float64)), np.abs(np.swapaxes(b32.astype(np.float64), 1, 2)))
     bound = kb * 2.0**-24 * magnitude + 1e-30
     got = p.float().cpu().numpy().astype(np.float64)
     if product_dtype == torch.float16:
         # one fp16 rounding of a value within `bound` of the exact sum
         bound = bound + np.abs(exact.astype(np.float64)) * 2.0**-11 + 2.0**-24
+    if product_dtype == torch.bfloat16:
+        # one bf16 rounding (8-bit significand)
+        bound = bound + np.abs(exact.astype(np.float64)) * 2.0**-8 + 2.0**-126
     assert np.all(np.abs(got - exact) <= bound)

@@ -38,9 +38,11 @@ def _kernels(assembly: str) -> dict[str, str]:
     return bodies
 
 
-def test_both_output_variants_are_checked(assembly) -> None:
-    names = _kernels(assembly)
-    assert any("ILi1E" in n for n in names) and any("ILi2E" in n for n in names), names
+def test_every_operand_and_product_variant_is_checked(assembly) -> None:
+    # template arguments <operand, products>: (fp16, fp16), (fp16, fp32), (bf16, bf16), (bf16, fp32)
+    names = set(_kernels(assembly))
+    for variant in ("ILi1ELi1E", "ILi1ELi2E", "ILi0ELi0E", "ILi0ELi2E"):
+        assert any(variant in n for n in names), (variant, names)
 
 
 def test_no_accumulator_access_inside_mfma_latency(assembly) -> None:
@@ -77,7 +79,8 @@ def test_main_loop_shape(assembly) -> None:
         ]
         count = lambda prefix: sum(op.startswith(prefix) for op in opcodes)  # noqa: E731
         # four slices per iteration: 64 MFMAs, 16 fragment reads, 8 refills each
-        assert count("v_mfma_f32_16x16x32_f16") == 256, name
+        mfma = "v_mfma_f32_16x16x32_bf16" if "ILi0E" in name.split("leaf_gemm_kernel", 1)[1][:6] else "v_mfma_f32_16x16x32_f16"
+        assert count(mfma) == 256, name
         assert count("ds_read_b128") == 64, name
         assert count("buffer_load_dwordx4") == 32, name
         assert count("s_barrier") == 4, name

@@ -54,14 +54,19 @@ def test_compiled_scheme_digests_match_verified_certificates() -> None:
 @pytest.mark.parametrize(
     ("call", "message"),
     (
-        (lambda lib: lib.fastmm_left_transform(0, 0, None, None, 4, 4, None), b"null pointer"),
-        (lambda lib: lib.fastmm_left_transform(0, 2, 16, 16, 4, 4, None), b"dtype"),
-        (lambda lib: lib.fastmm_weight_transform(0, 0, 16, 16, 0, 4, None), b"positive"),
-        (lambda lib: lib.fastmm_right_transform(1, 1, 16, 16, 4, -1, None), b"positive"),
-        (lambda lib: lib.fastmm_leaf_products(7, 16, 16, 16, 0, 2, 2, 2, None), b"fp16 or fp32"),
-        (lambda lib: lib.fastmm_leaf_products(0, 16, 16, 16, 1, 2, 2, 2, None), b"positive"),
-        (lambda lib: lib.fastmm_leaf_products(7, 16, 16, 16, 1, 1 << 20, 1 << 12, 2, None), b"2^31"),
-        (lambda lib: lib.fastmm_reconstruct(0, 0, 16, None, 0, 16, 4, 4, None), b"fp16 or fp32"),
+        (lambda lib: lib.fastmm_left_transform(0, 0, 1, None, None, 4, 4, None), b"null pointer"),
+        (lambda lib: lib.fastmm_left_transform(0, 2, 1, 16, 16, 4, 4, None), b"dtype"),
+        (lambda lib: lib.fastmm_left_transform(0, 0, 2, 16, 16, 4, 4, None), b"planes must be fp16 or bf16"),
+        (lambda lib: lib.fastmm_weight_transform(0, 0, 1, 16, 16, 0, 4, None), b"positive"),
+        (lambda lib: lib.fastmm_weight_transform(0, 0, 7, 16, 16, 4, 4, None), b"planes must be fp16 or bf16"),
+        (lambda lib: lib.fastmm_right_transform(1, 1, 1, 16, 16, 4, -1, None), b"positive"),
+        (lambda lib: lib.fastmm_right_transform(1, 1, 2, 16, 16, 4, 4, None), b"planes must be fp16 or bf16"),
+        (lambda lib: lib.fastmm_leaf_products(7, 2, 16, 16, 16, 2, 2, 2, 2, None), b"operands must be fp16 or bf16"),
+        (lambda lib: lib.fastmm_leaf_products(7, 1, 16, 16, 16, 0, 2, 2, 2, None), b"products must be fp32 or"),
+        (lambda lib: lib.fastmm_leaf_products(7, 0, 16, 16, 16, 1, 2, 2, 2, None), b"products must be fp32 or"),
+        (lambda lib: lib.fastmm_leaf_products(0, 1, 16, 16, 16, 1, 2, 2, 2, None), b"positive"),
+        (lambda lib: lib.fastmm_leaf_products(7, 1, 16, 16, 16, 1, 1 << 20, 1 << 12, 2, None), b"2^31"),
+        (lambda lib: lib.fastmm_reconstruct(0, 3, 16, None, 0, 16, 4, 4, None), b"fp16, bf16 or fp32"),
         (lambda lib: lib.fastmm_reconstruct(9, 1, 16, None, 0, 16, 4, 4, None), b"unknown scheme"),
     ),
 )

@@ -158,6 +158,38 @@ def test_fp16_store_matches_torch() -> None:
     assert np.array_equal(values.astype(np.float16).view(np.uint16), expected.view(np.uint16))
 
 
+@pytest.mark.parametrize("key", SCHEME_KEYS)
+def test_exact_small_integer_product_with_bf16_planes(key: str) -> None:
+    """bf16 planes of small integers are exact; with fp32 products the result is x @ W^T."""
+    rng = np.random.default_rng(23)
+    scheme = O.load_oracle_scheme(key)
+    x = rng.integers(-2, 3, (13, 17)).astype(np.float32)
+    w = rng.integers(-2, 3, (11, 17)).astype(np.float32)
+    exact = (x.astype(np.int64) @ w.T.astype(np.int64)).astype(np.float32)
+    out = O.linear(scheme, x, w, product_dtype="fp32", out_dtype="fp32", plane_dtype="bf16")
+    assert np.array_equal(out, exact)
+    a = O.left_transform(scheme, x, "bf16")
+    assert a.dtype == np.float32 and np.array_equal(a, O.left_transform(scheme, x).astype(np.float32))
+
+
+def test_bf16_plane_and_product_stores_match_torch() -> None:
+    """Planes and products in bf16 are the fp32 value rounded like ``Tensor.to(bfloat16)``."""
+    rng = np.random.default_rng(29)
+    scheme = O.load_oracle_scheme("rank7")
+    x = (rng.standard_normal((40, 36)) * 3).astype(np.float32)
+    planes = O.left_transform(scheme, x, "bf16")
+    fp32_planes = np.stack(
+        [np.asarray(p, dtype=np.float32) for p in O.evaluate_program(scheme.left, O._blocks(x, 2, 20, 18, False))]
+    )
+    expected = torch.from_numpy(fp32_planes).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(planes, expected)
+    a = planes[:, :, :16]
+    b = planes[:, :12, 2:18]
+    products = O.leaf_products(a, b, product_dtype="bf16")
+    exact32 = O.leaf_products(a, b, product_dtype="fp32")
+    assert np.array_equal(products, torch.from_numpy(exact32).to(torch.bfloat16).float().numpy())
+
+
 def test_leaf_products_f64_equal_exact_sum() -> None:
     rng = np.random.default_rng(4)
     a = rng.standard_normal((2, 3, 19)).astype(np.float16)

@@ -119,6 +119,12 @@ def test_byte_formulas_and_precision_pairs(monkeypatch) -> None:
         Rank48Plan(8, 8, 8, torch.device("cuda"), dtype=torch.float16)
     with pytest.raises(ValueError, match="does not support"):
         Rank7Plan(8, 8, 8, torch.device("cuda"), dtype=torch.bfloat16, compute_dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="does not support"):
+        Rank48Plan(8, 8, 8, torch.device("cuda"), dtype=torch.bfloat16, compute_dtype=torch.bfloat16)
+    # rank 49 offers BF16 leaves like the reference (runtime.py:852-858); bytes follow compute_dtype
+    bf16_leaves = Rank49Plan(5, 6, 7, torch.device("cuda"), dtype=torch.bfloat16, compute_dtype=torch.bfloat16)
+    assert bf16_leaves.compute_dtype == torch.bfloat16
+    assert bf16_leaves.workspace_bytes == rank49.workspace_bytes
 
 
 def test_memory_budget_is_checked_before_allocation(monkeypatch) -> None:
