@@ -4,8 +4,8 @@ Default workload: rank-7 dynamic plan, MLP-up
 linear M x K x N = 4096 x 4096 x 12288, x ~ N(0,1) BF16, weight[N, K] ~
 N(0, 1/K) BF16, no bias, FP16 leaves, output allocated per call, workspace
 reused. Inputs are generated on the CPU with a seeded torch.Generator and
-copied to HBM before timing. Other configurations: --config c3|c4|c5|c5-rank7|
-c5-rank49|c3-rank48.
+copied to HBM before timing. Other configurations: --config c3|c4|c4-bf16|c5|
+c5-rank7|c5-rank49|c3-rank48 (c4-bf16: the rank-49 plan with BF16 leaves).
 
 Prints ONE JSON line (the driver's contract). ``value`` is effective TFLOP/s
 = 2*M*N*K / t over the K timed steps; ``roofline`` is measured for the leaf
@@ -29,7 +29,7 @@ sys.path.insert(0, str(REPO_ROOT / "rdna3-fastmm_amd"))
 import torch  # noqa: E402
 
 METRIC = "ms and effective TFLOP/s per linear vs native BF16 GEMM (speedup), 1 MI355X"
-MFMA_FP16_PEAK_TFLOPS = 2500.0
+MFMA_16BIT_PEAK_TFLOPS = 2500.0  # dense FP16 and BF16 MFMA peak of MI355X
 HBM_PEAK_GBPS = 8000.0
 
 CONFIGS = {
@@ -41,6 +41,8 @@ CONFIGS = {
                       name="rank48-prepacked-8214x12288x4608"),
     "c4": dict(scheme="rank49", rows=19968, inner=4096, columns=16384, bias=True, prepacked=True,
                name="rank49-prepacked-mlp-up-19968x4096x16384-bias"),
+    "c4-bf16": dict(scheme="rank49", rows=19968, inner=4096, columns=16384, bias=True, prepacked=True,
+                    compute="bf16", name="rank49-bf16-leaves-prepacked-mlp-up-19968x4096x16384-bias"),
     "c5": dict(scheme="rank48", rows=8192, inner=8192, columns=8192, bias=False, prepacked=True,
                name="rank48-prepacked-square-8192"),
     "c5-rank7": dict(scheme="rank7", rows=8192, inner=8192, columns=8192, bias=False, prepacked=True,
@@ -87,12 +89,12 @@ def _median(values: list[float]) -> float:
     return ordered[len(ordered) // 2]
 
 
-def leaf_kernel_name(block_inner: int) -> str:
+def leaf_kernel_name(block_inner: int, compute: str) -> str:
     """The leaf-GEMM kernel fastmm_leaf_products runs for the bench shapes (aligned
-    fp16 products): the 16x16x32 kernel when Kb % 128 == 0, else the 32x32x16 one."""
+    16-bit products): the 16x16x32 kernel when Kb % 128 == 0, else the 32x32x16 one."""
     if block_inner % 128 == 0:
-        return "fastmm::mfma16::leaf_gemm_kernel<fp16> (fastmm_leaf_products)"
-    return "fastmm::fast::leaf_gemm_kernel<fp16> (fastmm_leaf_products)"
+        return f"fastmm::mfma16::leaf_gemm_kernel<{compute}, {compute}> (fastmm_leaf_products)"
+    return f"fastmm::fast::leaf_gemm_kernel<{compute}, {compute}> (fastmm_leaf_products)"
 
 
 def measured_traffic(config: str) -> float | None:
@@ -188,7 +190,8 @@ def main() -> int:
     m, k, n = cfg["rows"], cfg["inner"], cfg["columns"]
     flops = 2.0 * m * n * k
 
-    plan = PLAN_TYPES[cfg["scheme"]](m, k, n, device, dtype=torch.bfloat16, compute_dtype=torch.float16)
+    compute = torch.bfloat16 if cfg.get("compute") == "bf16" else torch.float16
+    plan = PLAN_TYPES[cfg["scheme"]](m, k, n, device, dtype=torch.bfloat16, compute_dtype=compute)
     workspace = plan.allocate_workspace(prepacked_right=cfg["prepacked"])
     packed = plan.pack_weight(w) if cfg["prepacked"] else None
     out = torch.empty((m, n), device=device, dtype=torch.bfloat16) if cfg["prepacked"] else None
@@ -269,7 +272,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16 in/out, fp16 MFMA leaves, fp32 accumulate",
+        "dtype": f"bf16 in/out, {'bf16' if compute == torch.bfloat16 else 'fp16'} MFMA leaves, fp32 accumulate",
         "data": "synthetic (seeded CPU torch.Generator: x~N(0,1), W~N(0,1/K), bias~N(0,0.02))",
         "config": {
             "workload": cfg["name"],
@@ -301,12 +304,12 @@ def main() -> int:
         "stages_ms": {name: round(v, 4) for name, v in stage_ms.items()},
         "packing_ms": round(pack_ms, 4),
         "roofline": {
-            "kernel": leaf_kernel_name(shape.block_inner),
+            "kernel": leaf_kernel_name(shape.block_inner, "bf16" if compute == torch.bfloat16 else "fp16"),
             "bound": "mfma",
             "achieved": round(leaf_tflops, 2),
-            "peak": MFMA_FP16_PEAK_TFLOPS,
+            "peak": MFMA_16BIT_PEAK_TFLOPS,
             "unit": "TFLOP/s",
-            "frac": round(leaf_tflops / MFMA_FP16_PEAK_TFLOPS, 4),
+            "frac": round(leaf_tflops / MFMA_16BIT_PEAK_TFLOPS, 4),
             "traffic": measured_traffic(args.config),
             "work_per_launch": f"2*R*Mb*Kb*Nb = {leaf_flops:.4e} flop",
         },
