@@ -369,16 +369,20 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
   // DMA mapping as in the 32x32 kernel: lane L of segment q writes row
   // 16*(4q + wave) + L/4, physical chunk L%4, and fetches the logical chunk
   // stored there (byte offsets within a K slab; the slab is the scalar
-  // offset). Rows past the leaf are clamped onto its last row, so every
-  // address lies inside the leaf's planes.
+  // offset). Rows past the leaf get the offset 2^31, which is out of range
+  // (num_records < 2^31, checked by the launcher) with or without the scalar
+  // offset added, so those lanes read nothing and their LDS slots are
+  // zero-filled: the padding rows then feed zeros to MFMAs whose results are
+  // never stored, which costs less energy than repeating real data.
+  constexpr unsigned kOutOfRange = 0x80000000u;
   const int seg_row = lane >> 2;
   unsigned a_off[SEGMENTS], b_off[SEGMENTS];
 #pragma unroll
   for (int q = 0; q < SEGMENTS; ++q) {
     const int row = (q * 4 + wave) * 16 + seg_row;
     const int chunk = (lane & 3) ^ ((row >> 2) & 3);
-    a_off[q] = static_cast<unsigned>((min(m0 + row, Mb - 1) * kSlab + chunk * 8) * 2);
-    b_off[q] = static_cast<unsigned>((min(n0 + row, Nb - 1) * kSlab + chunk * 8) * 2);
+    a_off[q] = m0 + row < Mb ? static_cast<unsigned>(((m0 + row) * kSlab + chunk * 8) * 2) : kOutOfRange;
+    b_off[q] = n0 + row < Nb ? static_cast<unsigned>(((n0 + row) * kSlab + chunk * 8) * 2) : kOutOfRange;
   }
   // Fragment reads: row l%16 of a 16-row block, logical chunk l/16. Two base
   // addresses (slots {0,1} and {2,3}) keep every offset an immediate.
@@ -734,7 +738,8 @@ bool fast_leaf_gemm_applies(const void* a, const void* b, const void* p, int64_t
 }
 
 // The 16x16x32 kernel additionally needs whole groups of four slices and leaf
-// planes whose byte offsets fit its 32-bit buffer addressing.
+// planes whose byte offsets fit its 32-bit buffer addressing; num_records (the
+// plane's bytes) stays below 2^31, the offset it uses for padding rows.
 bool mfma16_leaf_gemm_applies(int64_t mb, int64_t kb, int64_t nb) {
   return kb % (4 * mfma16::BK) == 0 && (mb + kTile) * kb * 2 <= INT32_MAX &&
          (nb + kTile) * kb * 2 <= INT32_MAX;
