@@ -374,15 +374,23 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
   // offset added, so those lanes read nothing and their LDS slots are
   // zero-filled: the padding rows then feed zeros to MFMAs whose results are
   // never stored, which costs less energy than repeating real data.
+  // A lane's rows in the four segments are r0 + 64q with r0 = 16*wave + L/4,
+  // and its swizzled chunk (L%4) ^ ((row/4)%4) is the same in all of them. A
+  // byte offset (row*32 + chunk*8)*2 is below 64*Mb exactly when row < Mb, so
+  // one per-lane base and a uniform limit give all eight offsets.
   constexpr unsigned kOutOfRange = 0x80000000u;
-  const int seg_row = lane >> 2;
+  constexpr unsigned kSegmentBytes = 64 * kSlab * 2;
+  const unsigned lane_base =
+      static_cast<unsigned>(((wave * 16 + (lane >> 2)) * kSlab + ((lane & 3) ^ ((lane >> 4) & 3)) * 8) * 2);
+  const unsigned a_first = lane_base + static_cast<unsigned>(m0 * kSlab * 2);
+  const unsigned b_first = lane_base + static_cast<unsigned>(n0 * kSlab * 2);
+  const unsigned a_limit = static_cast<unsigned>(Mb * kSlab * 2), b_limit = static_cast<unsigned>(Nb * kSlab * 2);
   unsigned a_off[SEGMENTS], b_off[SEGMENTS];
 #pragma unroll
   for (int q = 0; q < SEGMENTS; ++q) {
-    const int row = (q * 4 + wave) * 16 + seg_row;
-    const int chunk = (lane & 3) ^ ((row >> 2) & 3);
-    a_off[q] = m0 + row < Mb ? static_cast<unsigned>(((m0 + row) * kSlab + chunk * 8) * 2) : kOutOfRange;
-    b_off[q] = n0 + row < Nb ? static_cast<unsigned>(((n0 + row) * kSlab + chunk * 8) * 2) : kOutOfRange;
+    const unsigned a = a_first + q * kSegmentBytes, b = b_first + q * kSegmentBytes;
+    a_off[q] = a < a_limit ? a : kOutOfRange;
+    b_off[q] = b < b_limit ? b : kOutOfRange;
   }
   // Fragment reads: row l%16 of a 16-row block, logical chunk l/16. Two base
   // addresses (slots {0,1} and {2,3}) keep every offset an immediate.
@@ -528,17 +536,23 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
 #undef FASTMM_TIE
 
   const int64_t leaf_offset = static_cast<int64_t>(leaf) * Mb * Nb;
+  // The lane index is recomputed here (every lane is active): kept from the
+  // kernel's start, the row and column bases below would be live across the K
+  // loop and push accumulators into scratch memory.
+  int lane_now;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane_now));
+  const int out_row = wm * 128 + (lane_now & 15), out_col = wn * 128 + 4 * (lane_now >> 4);
   if constexpr (kOut == kFP32) {
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
-      const int row = m0 + wm * 128 + i * 16 + fr;
+      const int row = m0 + out_row + i * 16;
       if (row >= Mb) continue;
-      float* out_row = static_cast<float*>(P) + leaf_offset + static_cast<int64_t>(row) * Nb;
+      float* out_at = static_cast<float*>(P) + leaf_offset + static_cast<int64_t>(row) * Nb;
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
-        const int col = n0 + wn * 128 + j * 16 + 4 * fc;
+        const int col = n0 + out_col + j * 16;
         if (col < Nb) {
-          *reinterpret_cast<float4*>(out_row + col) =
+          *reinterpret_cast<float4*>(out_at + col) =
               make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
         }
       }
@@ -550,10 +564,10 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
     uint16_t* staged = reinterpret_cast<uint16_t*>(smem);
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
-      const int row = wm * 128 + i * 16 + fr;
+      const int row = out_row + i * 16;
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
-        const int col = wn * 128 + j * 16 + 4 * fc;
+        const int col = out_col + j * 16;
         uint16_t h[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) h[e] = from_f32<kOut>(acc[i][j][e]);

@@ -77,14 +77,25 @@ def _agprs(operands: str) -> set[int]:
     return registers
 
 
-def fence_violations(assembly: str) -> list[str]:
-    """Instructions that touch an asm MFMA's accumulator before a fence.
+WRITE_TO_MFMA_WAIT_STATES = 4
 
-    Scans each ``fastmm::mfma16`` kernel in program order: an MFMA marks its
-    destination AGPRs pending; three consecutive ``s_nop 7`` (the fence's 24
-    wait states) clear them; any other instruction naming a pending AGPR is a
-    violation. Branches are followed in layout order, which covers the loop
-    body, its exit and the straight-line tail the compiler emits.
+
+def fence_violations(assembly: str) -> list[str]:
+    """Compiler instructions that race an asm MFMA over an accumulator register.
+
+    Scans each ``fastmm::mfma16`` kernel in program order, in both directions:
+
+    * an MFMA marks its destination AGPRs pending; three consecutive
+      ``s_nop 7`` (the fence's 24 wait states) clear them; any other
+      instruction naming a pending AGPR is a violation (it would read or
+      overwrite a result still in flight);
+    * a non-MFMA write of an AGPR (``v_accvgpr_write/mov``, or a load into
+      one before its ``s_waitcnt``) must be at least
+      ``WRITE_TO_MFMA_WAIT_STATES`` wait states old when an MFMA reads that
+      register as its accumulator input.
+
+    Branches are followed in layout order, which covers loop bodies, their
+    exits and the straight-line tails the compiler emits.
     """
     violations: list[str] = []
     for match in ASM_CHECKED_KERNELS.finditer(assembly):
@@ -92,25 +103,45 @@ def fence_violations(assembly: str) -> list[str]:
         body = assembly[match.end():]
         body = body[: body.find("s_endpgm")]
         pending: set[int] = set()
+        written_at: dict[int, int] = {}  # AGPR -> wait-state clock of a VALU write
+        loaded: set[int] = set()  # AGPRs with a load in flight
+        clock = 0
         nops = 0
         for line in body.splitlines():
             text = line.split(";", 1)[0].strip()
             if not text or text.endswith(":") or text.startswith("."):
                 continue
             opcode, _, operands = text.partition(" ")
+            fields = [field.strip() for field in operands.split(",")]
             if opcode.startswith("v_mfma"):
-                destination = operands.split(",", 1)[0]
-                pending |= _agprs(destination)
+                accumulator_in = _agprs(fields[3]) if len(fields) > 3 else set()
+                recent = {r for r in accumulator_in if clock - written_at.get(r, -10**9) < WRITE_TO_MFMA_WAIT_STATES}
+                if recent or accumulator_in & loaded:
+                    violations.append(f"{name}: {text} (accumulator input written just before)")
+                pending |= _agprs(fields[0])
                 nops = 0
+                clock += 1
                 continue
             if opcode == "s_nop":
-                nops = nops + 1 if operands.strip() == "7" else 0
+                count = int(operands.strip() or 0)
+                clock += count + 1
+                nops = nops + 1 if count == 7 else 0
                 if nops >= 3:
                     pending.clear()
                 continue
             nops = 0
+            clock += 1
+            if opcode == "s_waitcnt":
+                loaded.clear()
+                continue
             if pending & _agprs(operands):
                 violations.append(f"{name}: {text}")
+            destination = _agprs(fields[0]) if fields else set()
+            if opcode.startswith("v_accvgpr_write") or opcode.startswith("v_accvgpr_mov"):
+                for register in destination:
+                    written_at[register] = clock
+            elif "load" in opcode:
+                loaded |= destination
     return violations
 
 

@@ -127,6 +127,11 @@ def test_reconstruct_bit_exact(key, shape, product_dtype) -> None:
         # several passes, ragged Mb / Nb tails, a single 8-column tile, rows not a multiple of 16
         (3, 513, 520, 128), (2, 17, 24, 256), (7, 256, 256, 2048), (2, 40, 8, 3072), (1, 1000, 776, 640),
         (4, 255, 264, 512),
+        # persistent 16x16x32 kernel (more tiles than one grid of 256 workgroups, Kb >= 256):
+        # one or two tiles per workgroup, ragged rows, one-row-tall last tiles, narrow
+        # columns, three or more tiles per workgroup
+        (7, 2048, 2304, 256), (2, 4107, 2304, 384), (48, 520, 512, 256), (17, 4000, 40, 256),
+        (49, 1024, 1024, 512),
     ),
 )
 @pytest.mark.parametrize(

@@ -68,6 +68,19 @@ def test_checker_on_synthetic_listing() -> None:
     assert _build.fence_violations(body) == ["_ZN6fastmm6mfma16kE: v_accvgpr_read_b32 v8, a2"]
 
 
+def test_checker_on_accumulator_input_written_just_before() -> None:
+    mfma = "\tv_mfma_f32_16x16x32_f16 a[4:7], v[0:3], v[4:7], a[0:3]\n"
+    tail = "\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_endpgm\n"
+    written = "_ZN6fastmm6mfma16kE:\n\tv_accvgpr_write_b32 a1, 0\n"
+    assert len(_build.fence_violations(written + mfma + tail)) == 1
+    # four wait states after the write: fine
+    assert _build.fence_violations(written + "\ts_nop 3\n" + mfma + tail) == []
+    # an AGPR load still in flight, then after its wait
+    loaded = "_ZN6fastmm6mfma16kE:\n\tscratch_load_dwordx4 a[0:3], off, off\n"
+    assert len(_build.fence_violations(loaded + "\ts_nop 7\n" + mfma + tail)) == 1
+    assert _build.fence_violations(loaded + "\ts_waitcnt vmcnt(0)\n\ts_nop 3\n" + mfma + tail) == []
+
+
 def test_main_loop_shape(assembly) -> None:
     for name, body in _kernels(assembly).items():
         loop = re.search(r"; =>This Inner Loop Header.*?s_cbranch_scc1", body, re.DOTALL)
