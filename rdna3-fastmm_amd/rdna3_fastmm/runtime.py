@@ -25,6 +25,8 @@ Differences that are visible to a caller, all deliberate:
 from __future__ import annotations
 
 from dataclasses import dataclass
+import json
+from pathlib import Path
 from typing import ClassVar
 
 import torch
@@ -194,12 +196,43 @@ def is_tested_runtime(device: torch.device) -> bool:
 
 # ------------------------------------------------------------- dispatch data
 
-# Shape families where a plan beat native BF16 torch.mm / F.linear on one
-# MI355X, with the measurement that showed it. The rewrite and
-# is_linear_recommended only ever select a family listed here. Measured so far
-# (bench.py, kernel-trace medians): rank-7 C3 0.87x, rank-48 8192^3 0.62x,
-# rank-49 C4 0.72x, rank-7 C2 0.51x of native -- no win yet, so the tables
-# below are empty and the graph rewrite leaves every Linear on native BF16.
+# Shape families where a plan beat native BF16 on one MI355X (reference
+# runtime.py:793-806, 831-838, 866-871 hold the RDNA3 tables). They are
+# measured, not modelled: ``python -m rdna3_fastmm.corpus --sweep`` times each
+# plan against native F.linear / torch.mm over a row sweep of a (K, N, bias)
+# pair, repeated on separate boxes, and a family is a run of swept rows where
+# every measurement beat native by the table's margin within the error bound.
+# Native hipBLASLt is fast on the MLP up projections (no family there) but
+# picks slow kernels for many row counts of the down projections, where the
+# plans' time stays smooth in M. The rewrite and is_linear_recommended only
+# ever select a family listed here.
+DISPATCH_TABLE_PATH = Path(__file__).resolve().parent / "dispatch" / "mi355x.json"
+_FAMILY_KEYS = {"scheme", "prepacked", "minimum_rows", "maximum_rows", "inner", "columns", "bias", "points",
+                "runs", "minimum_speedup"}
+
+
+def load_dispatch_table(path: Path = DISPATCH_TABLE_PATH) -> dict[tuple[str, bool], tuple[tuple[LinearShapeFamily, ...], dict[LinearShapeFamily, str]]]:
+    """(scheme, prepacked) -> (families, evidence per family) from a dispatch file."""
+    document = json.loads(Path(path).read_text())
+    if document.get("schema_version") != 1:
+        raise ValueError(f"{path}: unsupported dispatch schema {document.get('schema_version')!r}")
+    tables: dict[tuple[str, bool], tuple[list[LinearShapeFamily], dict[LinearShapeFamily, str]]] = {}
+    for index, entry in enumerate(document["families"]):
+        if set(entry) != _FAMILY_KEYS:
+            raise ValueError(f"{path}: families[{index}] has keys {sorted(entry)}")
+        if not (0 < entry["minimum_rows"] <= entry["maximum_rows"]) or entry["minimum_speedup"] < document["minimum_speedup"]:
+            raise ValueError(f"{path}: families[{index}] is not a measured win")
+        family = LinearShapeFamily(entry["minimum_rows"], entry["maximum_rows"], entry["inner"], entry["columns"],
+                                   entry["bias"])
+        mode = "prepacked" if entry["prepacked"] else "dynamic"
+        evidence = (f"{entry['scheme']} {mode}: >= {entry['minimum_speedup']}x native at {entry['points']} swept "
+                    f"row counts, {entry['runs']} runs each")
+        families, notes = tables.setdefault((entry["scheme"], entry["prepacked"]), ([], {}))
+        families.append(family)
+        notes[family] = evidence
+    return {key: (tuple(families), notes) for key, (families, notes) in tables.items()}
+
+
 MEASURED_WINS: dict[LinearShapeFamily, str] = {}
 
 
@@ -672,6 +705,20 @@ class Rank49Plan(_LinearPlan):
 
 
 PLAN_TYPES: dict[str, type[_LinearPlan]] = {"rank7": Rank7Plan, "rank48": Rank48Plan, "rank49": Rank49Plan}
+
+
+def _install_dispatch_table(path: Path = DISPATCH_TABLE_PATH) -> None:
+    for (scheme, prepacked), (families, notes) in load_dispatch_table(path).items():
+        plan_type = PLAN_TYPES[scheme]
+        if prepacked:
+            plan_type.prepacked_linear_shape_families = families
+        else:
+            plan_type.linear_shape_families = families
+        for family, note in notes.items():
+            MEASURED_WINS[family] = f"{MEASURED_WINS[family]}; {note}" if family in MEASURED_WINS else note
+
+
+_install_dispatch_table()
 
 Rank7Workspace = Workspace
 Rank49Workspace = Workspace

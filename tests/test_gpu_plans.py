@@ -241,3 +241,56 @@ def test_error_ratio_against_native_bf16(key) -> None:
         assert 1.2 < ratio < 1.9
     else:
         assert ratio <= 1.2
+
+
+def test_rewritten_graph_runs_a_measured_family() -> None:
+    """The shipped dispatch table selects rank 7 for the corpus's 4704 x 12288 -> 4608
+    down projection; the rewritten FX graph runs it within the error bound."""
+    from rdna3_fastmm.linear import RDNA3_RANK7_LINEAR_OP, rewrite_eligible_linears
+
+    class Down(torch.nn.Module):
+        def forward(self, input_tensor, weight):
+            return torch.nn.functional.linear(input_tensor, weight)
+
+    print("\n[case] rewritten graph, 4704x12288 -> 4608", flush=True)
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn((4704, 12288), generator=g).to(torch.bfloat16).to(DEVICE)
+    w = (torch.randn((4608, 12288), generator=g) / 12288**0.5).to(torch.bfloat16).to(DEVICE)
+    gm = torch.fx.symbolic_trace(Down())
+    for node, tensor in zip((n for n in gm.graph.nodes if n.op == "placeholder"), (x, w)):
+        node.meta["val"] = tensor
+    assert rewrite_eligible_linears(gm, [x, w]) == 1
+    gm.recompile()
+    assert RDNA3_RANK7_LINEAR_OP in {n.target for n in gm.graph.nodes if n.op == "call_function"}
+    out = gm(x, w)
+    exact = x.double() @ w.double().T
+    ratio = _rel(out, exact) / _rel(torch.nn.functional.linear(x, w), exact)
+    print(f"[ratio] rewritten rank7 {ratio:.3f}", flush=True)
+    assert ratio <= 1.2
+
+
+def test_external_mm_choice_runs_the_rank49_plan(monkeypatch) -> None:
+    """reference external_mm.py:34-48: an eligible FP16 mm runs the rank-49 dynamic plan."""
+    from rdna3_fastmm import external_mm
+    from rdna3_fastmm.runtime import Rank49Plan
+
+    calls = []
+    original = Rank49Plan.run
+    monkeypatch.setattr(Rank49Plan, "dynamic_shapes", frozenset({(200, 512, 520)}))
+    monkeypatch.setattr(Rank49Plan, "run", lambda self, *a, **k: calls.append(1) or original(self, *a, **k))
+    g = torch.Generator().manual_seed(5)
+    left = torch.randn((200, 512), generator=g).to(torch.float16).to(DEVICE)
+    right = (torch.randn((512, 520), generator=g) / 512**0.5).to(torch.float16).to(DEVICE)
+    out = torch.empty((200, 520), device=DEVICE, dtype=torch.float16)
+    with torch.inference_mode():
+        external_mm.rdna3_rank49_dynamic_v1_out(left, right, out=out)
+        assert calls == [1]
+        exact = left.double() @ right.double()
+        # the reference's mm bound (tests/test_rdna3.py:433-613); with an FP16 output,
+        # native's one 2^-11 rounding makes a ratio test meaningless for rank 49
+        assert _rel(out, exact) < 5e-3
+        # an unmeasured shape is torch.mm, bit for bit
+        other = torch.empty((200, 520), device=DEVICE, dtype=torch.float16)
+        external_mm.rdna3_rank49_dynamic_v1_out(left[:199].contiguous(), right, out=other[:199])
+        assert calls == [1]
+        assert torch.equal(other[:199], torch.mm(left[:199], right))

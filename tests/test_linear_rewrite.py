@@ -10,7 +10,7 @@ import pytest
 import torch
 from torch._subclasses.fake_tensor import FakeTensorMode
 
-from rdna3_fastmm import inductor, linear
+from rdna3_fastmm import external_mm, inductor, linear
 from rdna3_fastmm.linear import (
     RDNA3_LINEAR_OP,
     RDNA3_RANK7_LINEAR_OP,
@@ -105,11 +105,20 @@ def test_rewrite_rejects_non_contiguous_weight(measured) -> None:
 
 
 def test_shipped_tables_leave_graphs_untouched(monkeypatch) -> None:
-    """With no measured MI355X win the rewrite must not fire."""
+    """An MLP up projection has no measured MI355X win: the rewrite must not fire."""
     monkeypatch.setattr(torch.cuda, "mem_get_info", lambda device=None: (200 << 30, 288 << 30))
     (x, w), _ = fake((5120, 4608), (12288, 4608))
     gm = traced(Linear(), x, w)
     assert rewrite_eligible_linears(gm, [x, w]) == 0
+
+
+def test_shipped_tables_rewrite_a_measured_down_projection(monkeypatch) -> None:
+    """The corpus's 4704-token Ideogram MLP down projection is a measured rank-7 win."""
+    monkeypatch.setattr(torch.cuda, "mem_get_info", lambda device=None: (200 << 30, 288 << 30))
+    (x, w), _ = fake((4704, 12288), (4608, 12288))
+    gm = traced(Linear(), x, w)
+    assert rewrite_eligible_linears(gm, [x, w]) == 1
+    assert RDNA3_RANK7_LINEAR_OP in targets(gm)
 
 
 def test_operators_are_registered_with_fake_kernels() -> None:
@@ -121,8 +130,10 @@ def test_operators_are_registered_with_fake_kernels() -> None:
     assert tuple(out.shape) == (2, 3, 23) and out.dtype == torch.bfloat16
 
 
-def test_backend_disables_cudagraphs_only_after_a_rewrite(monkeypatch) -> None:
+def test_backend_adds_external_choice_and_disables_cudagraphs(monkeypatch) -> None:
+    """reference tests/test_inductor.py:34-67."""
     captured = {}
+    marker = object()
 
     def fake_compile(graph, example_inputs, options):
         captured["options"] = options
@@ -130,20 +141,63 @@ def test_backend_disables_cudagraphs_only_after_a_rewrite(monkeypatch) -> None:
 
     gm = torch.fx.symbolic_trace(lambda value: value.sin())
     monkeypatch.setattr(torch._inductor, "compile", fake_compile)
-    monkeypatch.setattr(inductor, "_enable_rewrite", lambda: True)
-    monkeypatch.setattr(inductor, "rewrite_eligible_linears", lambda graph, inputs: 1)
-    inductor.compile_backend(gm, [torch.randn(4)], mode="reduce-overhead")
-    assert captured["options"]["triton.cudagraphs"] is False
-
+    monkeypatch.setattr(inductor, "_enable_external_matmul", lambda: True)
     monkeypatch.setattr(inductor, "rewrite_eligible_linears", lambda graph, inputs: 0)
-    inductor.compile_backend(gm, [torch.randn(4)], mode="reduce-overhead")
-    assert captured["options"] == {"triton.cudagraphs": True}
+    inductor.compile_backend(gm, [torch.randn(4)], mode="reduce-overhead", options={"external_matmul": [marker]})
+    options = captured["options"]
+    assert options["external_matmul"] == [marker, external_mm.rdna3_rank49_dynamic_v1_out]
+    assert options["max_autotune_gemm"] is True and options["triton.cudagraphs"] is False
+    # the choice is added once
+    inductor.compile_backend(gm, [torch.randn(4)], options={"external_matmul": options["external_matmul"]})
+    assert captured["options"]["external_matmul"] == [marker, external_mm.rdna3_rank49_dynamic_v1_out]
+
+
+def test_external_mm_falls_back_for_ineligible_input() -> None:
+    """reference tests/test_inductor.py:21-31: CPU input, and a shape outside dynamic_shapes."""
+    left = torch.randn((7, 11), dtype=torch.float16)
+    right = torch.randn((11, 5), dtype=torch.float16)
+    out = torch.empty((7, 5), dtype=torch.float16)
+    with torch.inference_mode():
+        assert not external_mm.is_rank49_dynamic_eligible(left, right, out)
+        external_mm.rdna3_rank49_dynamic_v1_out(left, right, out=out)
+    torch.testing.assert_close(out, left @ right, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize(
+    "case",
+    ("grad", "dtype", "shape", "out_shape", "device", "noncontiguous", "unmeasured"),
+)
+def test_external_mm_eligibility(monkeypatch, case) -> None:
+    monkeypatch.setattr(Rank49Plan, "dynamic_shapes", frozenset({(64, 32, 48)}))
+    monkeypatch.setattr(external_mm, "is_tested_runtime", lambda device: True)
+    (left, right, out), mode = fake((64, 32), (32, 48), (64, 48), dtype=torch.float16)
+    with torch.inference_mode():
+        assert external_mm.is_rank49_dynamic_eligible(left, right, out)
+    with mode:
+        if case == "dtype":
+            left = left.to(torch.bfloat16)
+        elif case == "shape":
+            right = torch.empty((33, 48), dtype=torch.float16, device="cuda")
+        elif case == "out_shape":
+            out = torch.empty((64, 47), dtype=torch.float16, device="cuda")
+        elif case == "device":
+            out = torch.empty((64, 48), dtype=torch.float16)
+        elif case == "noncontiguous":
+            right = torch.empty((48, 32), dtype=torch.float16, device="cuda").t()
+        elif case == "unmeasured":
+            left = torch.empty((65, 32), dtype=torch.float16, device="cuda")
+            out = torch.empty((65, 48), dtype=torch.float16, device="cuda")
+    if case == "grad":
+        assert not external_mm.is_rank49_dynamic_eligible(left, right, out)
+        return
+    with torch.inference_mode():
+        assert not external_mm.is_rank49_dynamic_eligible(left, right, out)
 
 
 def test_backend_preserves_standard_inductor_when_runtime_is_unsupported(monkeypatch) -> None:
     captured = {}
     monkeypatch.setattr(torch._inductor, "compile", lambda g, i, options: captured.update(options=options))
-    monkeypatch.setattr(inductor, "_enable_rewrite", lambda: False)
+    monkeypatch.setattr(inductor, "_enable_external_matmul", lambda: False)
     inductor.compile_backend(torch.fx.symbolic_trace(lambda v: v.cos()), [torch.randn(4)], mode="reduce-overhead")
     assert captured["options"] == {"triton.cudagraphs": True}
 
