@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define FASTMM_ABI_VERSION 3
+#define FASTMM_ABI_VERSION 4
 
 #define FASTMM_OK 0
 #define FASTMM_ERROR_ARGUMENT 1    /* bad pointer, size, dtype or scheme */
@@ -62,6 +62,7 @@ extern "C" {
 #define FASTMM_SCHEME_RANK7 0  /* <2,2,2> rank 7  (certificate 2x2x2_rank7_15add) */
 #define FASTMM_SCHEME_RANK48 1 /* <4,4,4> rank 48 (certificate 4x4x4_rank48_accurate) */
 #define FASTMM_SCHEME_RANK49 2 /* <4,4,4> rank 49 (certificate 4x4x4_rank49_159add) */
+#define FASTMM_SCHEME_RANK343 3 /* <8,8,8> rank 343 (certificate 8x8x8_rank343_1661add); fp16 only */
 
 /* Library identity. */
 int fastmm_abi_version(void);

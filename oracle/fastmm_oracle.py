@@ -65,6 +65,7 @@ SCHEME_DIRECTORIES = {
     "rank7": "2x2x2_rank7_15add",
     "rank48": "4x4x4_rank48_accurate",
     "rank49": "4x4x4_rank49_159add",
+    "rank343": "8x8x8_rank343_1661add",
 }
 
 # An expression is ("sig", index) | ("add", a, b) | ("sub", a, b) | ("neg", a)
@@ -351,6 +352,43 @@ def reconstruct(
     return result
 
 
+def reconstruct_dense(
+    scheme: OracleScheme,
+    products: np.ndarray,
+    rows: int,
+    columns: int,
+    out_dtype: str = "fp16",
+) -> np.ndarray:
+    """The reference's rank-343 recombination as one dense dot.
+
+    reference ``tools/generate_triton_scheme.py:520-535`` (rank-major output
+    coefficients, row-major C blocks) and ``:547-624``
+    (``output_transform_mfma_kernel``): ``C block o = sum_r coeff[r][o] * P[r]``
+    with fp16 products and fp16 coefficients (-1, 0, 1) multiplied in a
+    ``tl.dot`` that accumulates in fp32, then stored as the output dtype. The
+    dot's fp32 summation order is unspecified; this restatement takes the
+    exact sum (every fp16 term is an integer multiple of 2^-24 below 2^16, so
+    343 of them sum exactly in fp64) rounded once to fp32.
+    """
+    s = scheme.size
+    _, mb, nb = products.shape
+    coefficients = np.array(program_matrix(scheme.output), dtype=object)
+    if any(c.denominator != 1 for c in coefficients.ravel()):
+        raise ValueError("dense recombination needs integer coefficients")
+    weights = coefficients.astype(np.int64).astype(np.float64)  # [s*s, R]
+    blocks = np.einsum("or,rmn->omn", weights, products.astype(np.float64)).astype(np.float32)
+    full = np.zeros((mb * s, nb * s), dtype=np.float32)
+    for c in range(s * s):
+        br, bc = divmod(c, s)
+        full[br * mb:(br + 1) * mb, bc * nb:(bc + 1) * nb] = blocks[c]
+    result = full[:rows, :columns]
+    if out_dtype == "fp16":
+        return result.astype(np.float16)
+    if out_dtype == "bf16":
+        return round_to_bf16(result)
+    return result
+
+
 def linear(
     scheme: OracleScheme,
     x: np.ndarray,
@@ -376,11 +414,18 @@ def matmul(
     accumulate: str = "f64",
     out_dtype: str = "fp16",
     plane_dtype: str = "fp16",
+    recombination: str = "program",
 ) -> np.ndarray:
-    """left[M, K] @ right[K, N] through the scheme (the plan ``run`` path)."""
+    """left[M, K] @ right[K, N] through the scheme (the plan ``run`` path).
+
+    ``recombination="dense"`` is the reference's rank-343 form
+    (``reconstruct_dense``); ``"program"`` evaluates the output circuit.
+    """
     a = left_transform(scheme, left, plane_dtype)
     b = right_transform(scheme, right, plane_dtype)
     p = leaf_products(a, b, product_dtype, accumulate)
+    if recombination == "dense":
+        return reconstruct_dense(scheme, p, left.shape[0], right.shape[1], out_dtype)
     return reconstruct(scheme, p, left.shape[0], right.shape[1], None, out_dtype)
 
 

@@ -13,6 +13,7 @@
 // other=0.0). Programs come from csrc/generated/*.h.
 #include "abi_common.h"
 #include "fastmm_device.h"
+#include "generated/rank343_8x8x8.h"
 #include "generated/rank48_4x4x4.h"
 #include "generated/rank49_4x4x4.h"
 #include "generated/rank7_2x2x2.h"
@@ -22,10 +23,25 @@ namespace fastmm {
 constexpr int kThreads = 256;
 
 // Elements per thread of the vector path: 8 (16-byte accesses) for the small
-// rank-7 program; 4 for the 48/49-output programs, whose live fp32 values
-// would otherwise spill.
+// rank-7 program; 4 for the 48/49-output programs and 2 for the 343-output
+// programs, whose live fp32 values would otherwise spill.
 template <class S>
-constexpr int vector_width() { return S::kRank <= 8 ? 8 : 4; }
+constexpr int vector_width() { return S::kRank <= 8 ? 8 : S::kRank <= 64 ? 4 : 2; }
+
+// The recombination reads R products per element: at R = 343 one element per
+// thread already fills the register file (two would spill).
+template <class S>
+constexpr int reconstruct_width() { return S::kRank <= 64 ? vector_width<S>() : 1; }
+
+// The 8x8-block schemes run in FP16 only (rank 343: FP16 operands, planes and
+// output, as the reference's only precision pair); other element types are
+// not instantiated for them.
+template <class S>
+constexpr bool fp16_only() { return S::kSize > 4; }
+
+// Threads per workgroup of the transform and recombination passes.
+template <class S>
+constexpr int block_threads() { return kThreads; }
 
 enum Side : int { kLeftSide = 0, kWeightSide = 1 };
 
@@ -43,14 +59,14 @@ enum Side : int { kLeftSide = 0, kWeightSide = 1 };
 // 128-byte line runs of every input row and writes RPW consecutive slab rows
 // (RPW * 64 bytes) per slab and plane.
 template <class S, int kSide, int kDType, int kPlane, int EPT, bool kVector, int kSpan>
-__global__ __launch_bounds__(kThreads) void direct_transform_kernel(
+__global__ __launch_bounds__(block_threads<S>()) void direct_transform_kernel(
     const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, int64_t src_rows,
     int64_t src_cols, int64_t rows_b, int64_t cols_b) {
   constexpr int s = S::kSize;
   const int64_t plane = rows_b * cols_b;
   int64_t row, col, at;
   if constexpr (kSpan == 0) {
-    at = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * EPT;
+    at = (static_cast<int64_t>(blockIdx.x) * block_threads<S>() + threadIdx.x) * EPT;
     if (at >= plane) return;
     row = at / cols_b;
     col = at - row * cols_b;
@@ -58,7 +74,7 @@ __global__ __launch_bounds__(kThreads) void direct_transform_kernel(
     constexpr int CPR = kSpan / EPT, RPW = 64 / CPR;  // chunks per row, rows per wave
     static_assert(CPR * RPW == 64 && kSpan % kSlab == 0, "a wave covers whole slab rows");
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    row = (static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + wave) * RPW + lane / CPR;
+    row = (static_cast<int64_t>(blockIdx.x) * (block_threads<S>() / 64) + wave) * RPW + lane / CPR;
     col = static_cast<int64_t>(blockIdx.y) * kSpan + (lane % CPR) * EPT;
     if (row >= rows_b) return;
     at = operand_offset<true>(row, col, rows_b, cols_b);
@@ -98,23 +114,32 @@ __global__ __launch_bounds__(kThreads) void direct_transform_kernel(
 constexpr int kTransposeTile = 32;
 static_assert(kTransposeTile == kSlab, "a transpose tile covers exactly one K slab");
 
+// Tile width in n: 32 columns of every input block for s <= 4 (s*s*32*33 fp32
+// = 67.6 KB of LDS at s = 4); 8 columns for s = 8, whose 64 input blocks
+// would need 270 KB at 32.
+template <class S>
+constexpr int transpose_columns() { return S::kSize <= 4 ? 32 : 8; }
+
 template <class S, int kDType, int kPlane, bool kSlabLayout>
 __global__ __launch_bounds__(kThreads) void transposed_right_kernel(
     const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, int64_t inner,
     int64_t columns, int64_t kb, int64_t nb) {
   constexpr int s = S::kSize;
   constexpr int T = kTransposeTile;
-  __shared__ float tile[s * s][T][T + 1];
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * T;
+  constexpr int TN = transpose_columns<S>();
+  constexpr int EK = T * TN / kThreads;  // k values per thread in the program pass
+  static_assert(EK >= 1 && T * TN % kThreads == 0, "the block covers the tile exactly");
+  __shared__ float tile[s * s][T][TN + 1];
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * TN;
   const int64_t k0 = static_cast<int64_t>(blockIdx.y) * T;
   const int tid = threadIdx.x;
-  const int nn = tid % T;
+  const int nn = tid % TN;
 #pragma unroll
   for (int j = 0; j < s * s; ++j) {
     const int64_t block_k = j / s, block_n = j % s;
 #pragma unroll
-    for (int pass = 0; pass < T * T / kThreads; ++pass) {
-      const int kk = tid / T + pass * (kThreads / T);
+    for (int pass = 0; pass < T * TN / kThreads; ++pass) {
+      const int kk = tid / TN + pass * (kThreads / TN);
       const int64_t k = k0 + kk, n = n0 + nn;
       const int64_t src_row = block_k * kb + k, src_col = block_n * nb + n;
       float value = 0.0f;
@@ -125,25 +150,25 @@ __global__ __launch_bounds__(kThreads) void transposed_right_kernel(
     }
   }
   __syncthreads();
-  const int n_local = tid / 8;
-  const int k_local = (tid % 8) * 4;
-  auto load = [&](int j) -> Vec<4> {
-    Vec<4> v;
+  const int n_local = tid / (T / EK);
+  const int k_local = (tid % (T / EK)) * EK;
+  auto load = [&](int j) -> Vec<EK> {
+    Vec<EK> v;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v.v[e] = tile[j][k_local + e][n_local];
+    for (int e = 0; e < EK; ++e) v.v[e] = tile[j][k_local + e][n_local];
     return v;
   };
   const int64_t n = n0 + n_local;
   const int64_t k = k0 + k_local;
-  auto store = [&](int r, const Vec<4>& v) {
+  auto store = [&](int r, const Vec<EK>& v) {
     if (n >= nb) return;
     uint16_t* p = dst + static_cast<int64_t>(r) * nb * kb + operand_offset<kSlabLayout>(n, k, nb, kb);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int e = 0; e < EK; ++e) {
       if (k + e < kb) p[e] = from_f32<kPlane>(v.v[e]);
     }
   };
-  S::template right<Vec<4>>(load, store);
+  S::template right<Vec<EK>>(load, store);
 }
 
 // C = output(P planes) (+ bias), stored as kOut. One thread: EPT consecutive
@@ -174,12 +199,12 @@ __device__ __forceinline__ Vec<EPT> load_product(const void* products, int64_t o
 }
 
 template <class S, int kProd, int kOut, int EPT, bool kVector, bool kBias>
-__global__ __launch_bounds__(kThreads) void reconstruct_kernel(
+__global__ __launch_bounds__(block_threads<S>()) void reconstruct_kernel(
     const void* __restrict__ products, const uint16_t* __restrict__ bias,
     uint16_t* __restrict__ out, int64_t rows, int64_t cols, int64_t rows_b, int64_t cols_b) {
   constexpr int s = S::kSize;
   const int64_t plane = rows_b * cols_b;
-  const int64_t first = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * EPT;
+  const int64_t first = (static_cast<int64_t>(blockIdx.x) * block_threads<S>() + threadIdx.x) * EPT;
   if (first >= plane) return;
   const int64_t row = first / cols_b;
   const int64_t col = first - row * cols_b;
@@ -219,6 +244,7 @@ int launch_direct(int side, int dtype, int plane_dtype, const void* src, void* d
                   int64_t src_cols, hipStream_t stream) {
   constexpr int s = S::kSize;
   constexpr int W = vector_width<S>();
+  constexpr int B = block_threads<S>();
   const int64_t rows_b = ceil_div(src_rows, s);
   const int64_t cols_b = ceil_div(src_cols, s);
   const bool vector = src_cols % (s * W) == 0 && aligned_to(src, 2 * W) && aligned_to(dst, 2 * W);
@@ -231,19 +257,19 @@ int launch_direct(int side, int dtype, int plane_dtype, const void* src, void* d
   }
   // 1D grid over the plane (row-major) or 2D grid of (4 waves x RPW rows) x kSpan columns
   auto grid_for = [&](int ept, int kspan) {
-    if (kspan == 0) return dim3(static_cast<unsigned>(ceil_div(plane, static_cast<int64_t>(kThreads) * ept)));
-    const int64_t rows_per_block = static_cast<int64_t>(kThreads / 64) * (64 / (kspan / ept));
+    if (kspan == 0) return dim3(static_cast<unsigned>(ceil_div(plane, static_cast<int64_t>(B) * ept)));
+    const int64_t rows_per_block = static_cast<int64_t>(B / 64) * (64 / (kspan / ept));
     return dim3(static_cast<unsigned>(ceil_div(rows_b, rows_per_block)), static_cast<unsigned>(cols_b / kspan));
   };
 #define FASTMM_DIRECT_LAYOUT(SIDE, DT, PL, SPAN)                                              \
   do {                                                                                        \
     if (vector)                                                                               \
-      direct_transform_kernel<S, SIDE, DT, PL, W, true, SPAN><<<grid_for(W, SPAN), kThreads, 0, \
+      direct_transform_kernel<S, SIDE, DT, PL, W, true, SPAN><<<grid_for(W, SPAN), B, 0,        \
                                                                  stream>>>(in, out, src_rows,  \
                                                                            src_cols, rows_b,   \
                                                                            cols_b);            \
     else                                                                                      \
-      direct_transform_kernel<S, SIDE, DT, PL, 1, false, SPAN><<<grid_for(1, SPAN), kThreads,   \
+      direct_transform_kernel<S, SIDE, DT, PL, 1, false, SPAN><<<grid_for(1, SPAN), B,          \
                                                                   0, stream>>>(in, out,        \
                                                                                src_rows,       \
                                                                                src_cols,       \
@@ -260,7 +286,14 @@ int launch_direct(int side, int dtype, int plane_dtype, const void* src, void* d
     if (plane_dtype == kBF16) FASTMM_DIRECT_PLANE(SIDE, DT, kBF16);                           \
     else FASTMM_DIRECT_PLANE(SIDE, DT, kFP16);                                                \
   } while (0)
-  if (side == kLeftSide) {
+  if constexpr (fp16_only<S>()) {
+    if (dtype != kFP16 || plane_dtype != kFP16) {
+      return fail(FASTMM_ERROR_UNSUPPORTED, "transform: the %dx%d-block scheme takes fp16 input and planes",
+                  s, s);
+    }
+    if (side == kLeftSide) FASTMM_DIRECT_PLANE(kLeftSide, kFP16, kFP16);
+    else FASTMM_DIRECT_PLANE(kWeightSide, kFP16, kFP16);
+  } else if (side == kLeftSide) {
     if (dtype == kBF16) FASTMM_DIRECT(kLeftSide, kBF16);
     else FASTMM_DIRECT(kLeftSide, kFP16);
   } else {
@@ -279,7 +312,7 @@ int launch_transposed(int dtype, int plane_dtype, const void* src, void* dst, in
   constexpr int s = S::kSize;
   const int64_t kb = ceil_div(inner, s);
   const int64_t nb = ceil_div(columns, s);
-  const dim3 grid(static_cast<unsigned>(ceil_div(nb, kTransposeTile)),
+  const dim3 grid(static_cast<unsigned>(ceil_div(nb, static_cast<int64_t>(transpose_columns<S>()))),
                   static_cast<unsigned>(ceil_div(kb, kTransposeTile)));
   const uint16_t* in = static_cast<const uint16_t*>(src);
   uint16_t* out = static_cast<uint16_t*>(dst);
@@ -291,7 +324,13 @@ int launch_transposed(int dtype, int plane_dtype, const void* src, void* dst, in
     else transposed_right_kernel<S, DT, PL, false><<<grid, kThreads, 0, stream>>>(in, out, inner,       \
                                                                                    columns, kb, nb);     \
   } while (0)
-  if (dtype == kBF16) {
+  if constexpr (fp16_only<S>()) {
+    if (dtype != kFP16 || plane_dtype != kFP16) {
+      return fail(FASTMM_ERROR_UNSUPPORTED, "right transform: the %dx%d-block scheme takes fp16 input and planes",
+                  s, s);
+    }
+    FASTMM_TRANSPOSED(kFP16, kFP16);
+  } else if (dtype == kBF16) {
     if (plane_dtype == kBF16) FASTMM_TRANSPOSED(kBF16, kBF16);
     else FASTMM_TRANSPOSED(kBF16, kFP16);
   } else {
@@ -306,13 +345,13 @@ template <class S, int kProd, int kOut, bool kBias>
 void launch_reconstruct_typed(bool vector, dim3 grid, hipStream_t stream, const void* products,
                               const uint16_t* bias, uint16_t* out, int64_t rows, int64_t cols,
                               int64_t rows_b, int64_t cols_b) {
-  constexpr int W = vector_width<S>();
+  constexpr int W = reconstruct_width<S>();
   if (vector) {
     reconstruct_kernel<S, kProd, kOut, W, true, kBias>
-        <<<grid, kThreads, 0, stream>>>(products, bias, out, rows, cols, rows_b, cols_b);
+        <<<grid, block_threads<S>(), 0, stream>>>(products, bias, out, rows, cols, rows_b, cols_b);
   } else {
     reconstruct_kernel<S, kProd, kOut, 1, false, kBias>
-        <<<grid, kThreads, 0, stream>>>(products, bias, out, rows, cols, rows_b, cols_b);
+        <<<grid, block_threads<S>(), 0, stream>>>(products, bias, out, rows, cols, rows_b, cols_b);
   }
 }
 
@@ -320,14 +359,14 @@ template <class S>
 int launch_reconstruct(int products_dtype, const void* products, const void* bias, int dtype,
                        void* output, int64_t rows, int64_t cols, hipStream_t stream) {
   constexpr int s = S::kSize;
-  constexpr int W = vector_width<S>();
+  constexpr int W = reconstruct_width<S>();
   const int64_t rows_b = ceil_div(rows, s);
   const int64_t cols_b = ceil_div(cols, s);
   const int product_bytes = products_dtype == kFP32 ? 4 : 2;
   const bool vector = cols % (s * W) == 0 && aligned_to(products, product_bytes * W) &&
                       aligned_to(output, 2 * W) && (bias == nullptr || aligned_to(bias, 2 * W));
   const int64_t plane = rows_b * cols_b;
-  const int64_t per_block = static_cast<int64_t>(kThreads) * (vector ? W : 1);
+  const int64_t per_block = static_cast<int64_t>(block_threads<S>()) * (vector ? W : 1);
   const dim3 grid(static_cast<unsigned>(ceil_div(plane, per_block)));
   const uint16_t* b = static_cast<const uint16_t*>(bias);
   uint16_t* out = static_cast<uint16_t*>(output);
@@ -340,7 +379,14 @@ int launch_reconstruct(int products_dtype, const void* products, const void* bia
       launch_reconstruct_typed<S, PROD, OUT, false>(vector, grid, stream, products, b, out,     \
                                                     rows, cols, rows_b, cols_b);                \
   } while (0)
-  if (products_dtype == kFP32) {
+  if constexpr (fp16_only<S>()) {
+    if (dtype != kFP16 || products_dtype == kBF16) {
+      return fail(FASTMM_ERROR_UNSUPPORTED,
+                  "reconstruct: the %dx%d-block scheme takes fp16 or fp32 products and an fp16 output", s, s);
+    }
+    if (products_dtype == kFP32) FASTMM_RECON(kFP32, kFP16);
+    else FASTMM_RECON(kFP16, kFP16);
+  } else if (products_dtype == kFP32) {
     if (dtype == kBF16) FASTMM_RECON(kFP32, kBF16);
     else FASTMM_RECON(kFP32, kFP16);
   } else if (products_dtype == kBF16) {
@@ -361,6 +407,7 @@ int with_scheme(int scheme, F&& f) {
     case FASTMM_SCHEME_RANK7: return f.template operator()<SchemeRank7>();
     case FASTMM_SCHEME_RANK48: return f.template operator()<SchemeRank48>();
     case FASTMM_SCHEME_RANK49: return f.template operator()<SchemeRank49>();
+    case FASTMM_SCHEME_RANK343: return f.template operator()<SchemeRank343>();
     default: return fail(FASTMM_ERROR_ARGUMENT, "unknown scheme id %d", scheme);
   }
 }
@@ -405,6 +452,7 @@ extern "C" const char* fastmm_scheme_sha256(int scheme) {
     case FASTMM_SCHEME_RANK7: return SchemeRank7::kCertificateSha256;
     case FASTMM_SCHEME_RANK48: return SchemeRank48::kCertificateSha256;
     case FASTMM_SCHEME_RANK49: return SchemeRank49::kCertificateSha256;
+    case FASTMM_SCHEME_RANK343: return SchemeRank343::kCertificateSha256;
     default: return nullptr;
   }
 }

@@ -15,7 +15,7 @@ import torch
 
 from ._build import LIBRARY_PATH
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 BF16, FP16, FP32 = 0, 1, 2
 _DTYPE_CODES = {torch.bfloat16: BF16, torch.float16: FP16, torch.float32: FP32}

@@ -704,6 +704,24 @@ class Rank49Plan(_LinearPlan):
     )
 
 
+class Rank343Plan(_Plan):
+    """<8,8,8> rank 343 (1661 additions), FP16 ``mm`` only; reference runtime.py:883-962.
+
+    Only the ``mm`` path (``pack_right``, ``run``, ``run_packed``): the reference
+    offers no Linear plan for it. The recombination evaluates the certificate's
+    output circuit in fp32, like the other schemes; the reference evaluates the
+    same integer combination as one dense FP16 dot with fp32 accumulation
+    (``MFMA_OUTPUT_COEFFICIENTS``), so the two agree up to fp32 summation order.
+    ``prepacked_shapes`` and ``dynamic_shapes`` hold MI355X-measured wins only.
+    """
+
+    algorithm = "rank343-mfma-v1"
+    scheme_key = "rank343"
+    rank = 343
+    scheme_size = 8
+    precision_pairs = frozenset({(torch.float16, torch.float16)})
+
+
 PLAN_TYPES: dict[str, type[_LinearPlan]] = {"rank7": Rank7Plan, "rank48": Rank48Plan, "rank49": Rank49Plan}
 
 
@@ -722,3 +740,4 @@ _install_dispatch_table()
 
 Rank7Workspace = Workspace
 Rank49Workspace = Workspace
+Rank343Workspace = Workspace

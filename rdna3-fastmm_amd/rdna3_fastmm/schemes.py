@@ -74,6 +74,10 @@ _ENTRIES = {
         "rank49_4x4x4", "rank49-v1", "4x4x4_rank49_159add", "reduced",
         "a3c4121dfd09607045255628dd94b60133c24c46b65f1089e89c6564ba522561", 2,
     ),
+    "rank343": _Entry(
+        "rank343_8x8x8", "rank343-mfma-v1", "8x8x8_rank343_1661add", "reduced",
+        "c7afccb09f8491e484af1696c25c809757c4af649ee7220e79f25d1c7afe3955", 3,
+    ),
 }
 
 SCHEME_KEYS = tuple(_ENTRIES)

@@ -33,7 +33,7 @@ def test_vendored_files_match_pinned_digests() -> None:
         digest, name = line.split()
         assert hashlib.sha256((CERTIFICATE_ROOT / name).read_bytes()).hexdigest() == digest
         checked += 1
-    assert checked == 9
+    assert checked == 11
 
 
 @pytest.mark.parametrize(
@@ -69,6 +69,30 @@ def test_rank49_certificate_is_exact() -> None:
     assert summary.side_additions == (42, 42, 75)
     assert summary.additions == 159
     assert summary.tensor_entries == 64
+
+
+def test_rank343_certificate_is_exact() -> None:
+    """Counts stated in the certificate's README (8x8x8_rank343_1661add): 343
+    multiplications, 1661 additions, directional costs 462, 456 and 743, every
+    edge +-1; the upstream file's SHA-256."""
+    path = RANK49.parent.parent / "8x8x8_rank343_1661add" / "certificate.json"
+    assert hashlib.sha256(path.read_bytes()).hexdigest() == (
+        "c7afccb09f8491e484af1696c25c809757c4af649ee7220e79f25d1c7afe3955"
+    )
+    source = load_reduced_scheme(path)
+    summary = verify_reduced_scheme(source)
+    assert summary.dimensions == (8, 8, 8)
+    assert summary.rank == 343
+    assert summary.side_additions == (462, 456, 743)
+    assert summary.additions == 1661
+    assert {term["value"] for key in ("u_fresh", "u", "v_fresh", "v", "w_fresh", "w")
+            for expression in source[key] for term in expression} == {-1, 1}
+    # the reference's MFMA recombination table: 343 rows of 64 coefficients in {-1, 0, 1}
+    # (tests/test_generate_triton_scheme.py:262-281)
+    expanded = load_expanded_scheme(path)
+    assert len(expanded.output_coefficients) == 64
+    assert all(len(row) == 343 for row in expanded.output_coefficients)
+    assert {value for row in expanded.output_coefficients for value in row} == {-1, 0, 1}
 
 
 def test_rank7_certificate_is_exact() -> None:

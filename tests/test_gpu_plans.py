@@ -294,3 +294,41 @@ def test_external_mm_choice_runs_the_rank49_plan(monkeypatch) -> None:
         external_mm.rdna3_rank49_dynamic_v1_out(left[:199].contiguous(), right, out=other[:199])
         assert calls == [1]
         assert torch.equal(other[:199], torch.mm(left[:199], right))
+
+
+def test_rank343_dynamic_and_packed_match_exact_small_product() -> None:
+    """reference test_rdna3.py:726-752: small integers stay exact through rank 343."""
+    from rdna3_fastmm.runtime import Rank343Plan
+
+    torch.manual_seed(17)
+    for shape in ((5, 6, 7), (37, 29, 41), (64, 64, 64)):
+        print(f"\n[case] rank343 exact {shape}", flush=True)
+        left = torch.randint(-2, 3, shape[:2], device=DEVICE, dtype=torch.float16)
+        right = torch.randint(-2, 3, shape[1:], device=DEVICE, dtype=torch.float16)
+        reference = (left.float() @ right.float()).half()
+        plan = Rank343Plan(*shape, device=DEVICE)
+        packed = plan.pack_right(right, max_free_memory_fraction=0.1)
+        dynamic = plan.run(left, right, plan.allocate_workspace(max_free_memory_fraction=0.1))
+        prepacked = plan.run_packed(left, packed, plan.allocate_workspace(0.1, prepacked_right=True))
+        assert torch.equal(dynamic, reference) and torch.equal(prepacked, reference)
+
+
+def test_rank343_matches_oracle_within_the_mm_bound() -> None:
+    """Random FP16 operands: equal to the oracle's circuit evaluation up to leaf fp32
+    accumulation, and inside the reference's mm bound (rel-L2 < 5e-3)."""
+    from rdna3_fastmm.runtime import Rank343Plan
+
+    m, k, n = 200, 264, 136
+    print(f"\n[case] rank343 oracle {m}x{k}x{n}", flush=True)
+    g = torch.Generator().manual_seed(23)
+    left = torch.randn((m, k), generator=g).to(torch.float16)
+    right = (torch.randn((k, n), generator=g) / k**0.5).to(torch.float16)
+    plan = Rank343Plan(m, k, n, device=DEVICE)
+    out = plan.run(left.to(DEVICE), right.to(DEVICE), plan.allocate_workspace(0.1)).float().cpu().numpy()
+    scheme = O.load_oracle_scheme("rank343")
+    circuit = O.matmul(scheme, left.float().numpy(), right.float().numpy()).astype(np.float32)
+    dense = O.matmul(scheme, left.float().numpy(), right.float().numpy(), recombination="dense").astype(np.float32)
+    exact = left.double().numpy() @ right.double().numpy()
+    for expected in (circuit, dense):
+        assert np.linalg.norm(out - expected) <= 0.2 * np.linalg.norm(expected - exact)
+    assert np.linalg.norm(out - exact) / np.linalg.norm(exact) < 5e-3

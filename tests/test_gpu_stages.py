@@ -53,6 +53,11 @@ def _bits(t: torch.Tensor) -> np.ndarray:
     return t.detach().cpu().view(torch.int16).numpy()
 
 
+def _fp16_only(scheme) -> bool:
+    """The 8x8-block scheme (rank 343) runs FP16 operands, planes and outputs only."""
+    return scheme.size > 4
+
+
 def _plane_bits(planes: np.ndarray, plane_dtype: str) -> np.ndarray:
     if plane_dtype == "bf16":
         return O.round_to_bf16(planes).view(np.int16)
@@ -76,6 +81,12 @@ def test_transforms_bit_exact(key, shape, dtype, plane_dtype) -> None:
     a = torch.empty(operand_shape(r, mb, kb), device=DEVICE, dtype=planes)
     b = torch.empty(operand_shape(r, nb, kb), device=DEVICE, dtype=planes)
     b2 = torch.empty_like(b)
+    if _fp16_only(scheme) and (dtype != torch.float16 or plane_dtype != "fp16"):
+        for stage, args in ((_stages.left_transform, (xg, a, m, k)), (_stages.weight_transform, (wg, b, n, k)),
+                            (_stages.right_transform, (wg.t().contiguous(), b2, k, n))):
+            with pytest.raises(RuntimeError, match="takes fp16 input and planes"):
+                stage(scheme, *args)
+        return
     _stages.left_transform(scheme, xg, a, m, k)
     _stages.weight_transform(scheme, wg, b, n, k)
     right = wg.t().contiguous()
@@ -101,6 +112,11 @@ def test_reconstruct_bit_exact(key, shape, product_dtype) -> None:
     products = torch.randn((r, _ceil(m, s), _ceil(n, s)), generator=g).to(product_dtype)
     for dtype in DTYPES:
         bias = (torch.randn((n,), generator=g) * 0.1).to(dtype)
+        if _fp16_only(scheme) and (dtype != torch.float16 or product_dtype == torch.bfloat16):
+            out = torch.empty((m, n), device=DEVICE, dtype=dtype)
+            with pytest.raises(RuntimeError, match="fp16 or fp32 products and an fp16 output"):
+                _stages.reconstruct(scheme, products.to(DEVICE), None, out, m, n)
+            continue
         for use_bias in (False, True):
             out = torch.empty((m, n), device=DEVICE, dtype=dtype)
             _stages.reconstruct(scheme, products.to(DEVICE), bias.to(DEVICE) if use_bias else None, out, m, n)
@@ -127,9 +143,8 @@ def test_reconstruct_bit_exact(key, shape, product_dtype) -> None:
         # several passes, ragged Mb / Nb tails, a single 8-column tile, rows not a multiple of 16
         (3, 513, 520, 128), (2, 17, 24, 256), (7, 256, 256, 2048), (2, 40, 8, 3072), (1, 1000, 776, 640),
         (4, 255, 264, 512),
-        # persistent 16x16x32 kernel (more tiles than one grid of 256 workgroups, Kb >= 256):
-        # one or two tiles per workgroup, ragged rows, one-row-tall last tiles, narrow
-        # columns, three or more tiles per workgroup
+        # more tiles than one wave of 256 workgroups: ragged rows, one-row-tall last tiles,
+        # narrow columns, many leaves
         (7, 2048, 2304, 256), (2, 4107, 2304, 384), (48, 520, 512, 256), (17, 4000, 40, 256),
         (49, 1024, 1024, 512),
     ),

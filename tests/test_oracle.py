@@ -41,10 +41,28 @@ def _brent_ok(scheme: O.OracleScheme) -> bool:
     return True
 
 
+def _brent_integer_ok(scheme: O.OracleScheme) -> bool:
+    """The full Brent tensor with integer arithmetic (numpy), for large schemes."""
+    s = scheme.size
+    u, v, w = (np.array(O.program_matrix(p), dtype=object) for p in (scheme.left, scheme.right, scheme.output))
+    if any(c.denominator != 1 for m in (u, v, w) for c in m.ravel()):
+        return False
+    u, v, w = (m.astype(np.int64) for m in (u, v, w))
+    tensor = np.einsum("ra,rb,cr->abc", u, v, w)  # a = (i, k), b = (k2, j), c = (i2, j2)
+    expected = np.zeros((s * s, s * s, s * s), dtype=np.int64)
+    for i in range(s):
+        for k in range(s):
+            for j in range(s):
+                expected[i * s + k, k * s + j, i * s + j] = 1
+    return bool(np.array_equal(tensor, expected))
+
+
 @pytest.mark.parametrize("key", SCHEME_KEYS)
 def test_oracle_scheme_satisfies_brent_identity(key: str) -> None:
     scheme = O.load_oracle_scheme(key)
-    if scheme.size == 4:
+    if scheme.size == 8:
+        assert _brent_integer_ok(scheme)
+    elif scheme.size == 4:
         # The 4096-entry brute force is slow in pure Python; the rank-7 case runs
         # in full and the s=4 schemes through the cheaper bilinear check below.
         rng = np.random.default_rng(3)
@@ -114,6 +132,35 @@ def test_planted_sign_error_is_caught() -> None:
     xr, wr = rng.standard_normal((8, 8)), rng.standard_normal((8, 8))
     assert np.max(np.abs(O.linear_float64(broken, xr, wr) - xr @ wr.T)) > 1e-3
     assert not _brent_ok(broken)
+    # the integer check used for the 8x8-block scheme agrees on both
+    assert _brent_integer_ok(scheme) and not _brent_integer_ok(broken)
+    broken343 = deepcopy(O.load_oracle_scheme("rank343"))
+    signal, node = broken343.left.assignments[-1]
+    broken343.left.assignments[-1] = (signal, ("neg", node))
+    assert not _brent_integer_ok(broken343)
+
+
+def test_rank343_dense_recombination_matches_the_circuit() -> None:
+    """The reference's dense rank-343 recombination (one fp32-accumulated dot) and the
+    certificate's output circuit evaluated in fp32 agree to one fp16 rounding; on
+    small integers both are exact."""
+    scheme = O.load_oracle_scheme("rank343")
+    rng = np.random.default_rng(7)
+    products = rng.standard_normal((343, 6, 5)).astype(np.float16)
+    dense = O.reconstruct_dense(scheme, products, 45, 38, out_dtype="fp32")
+    circuit = O.reconstruct(scheme, products, 45, 38, out_dtype="fp32")
+    # fp32 summation-order differences only: far below one fp16 ulp of the output
+    scale = np.abs(np.einsum("or,rmn->omn", np.abs(np.array(O.program_matrix(scheme.output), dtype=np.float64)),
+                             np.abs(products.astype(np.float64)))).max()
+    assert np.max(np.abs(dense - circuit)) <= 343 * 2.0**-24 * scale
+    assert np.max(np.abs(dense.astype(np.float16).astype(np.float32) -
+                         circuit.astype(np.float16).astype(np.float32))) <= 2.0**-10 * np.abs(dense).max()
+    x = rng.integers(-2, 3, (37, 29)).astype(np.float16)
+    y = rng.integers(-2, 3, (29, 41)).astype(np.float16)
+    exact = (x.astype(np.int64) @ y.astype(np.int64)).astype(np.float16)
+    for recombination in ("dense", "program"):
+        got = O.matmul(scheme, x.astype(np.float32), y.astype(np.float32), recombination=recombination)
+        assert np.array_equal(got, exact), recombination
 
 
 def test_planted_transposed_weight_is_caught() -> None:

@@ -121,6 +121,12 @@ def test_byte_formulas_and_precision_pairs(monkeypatch) -> None:
         Rank7Plan(8, 8, 8, torch.device("cuda"), dtype=torch.bfloat16, compute_dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="does not support"):
         Rank48Plan(8, 8, 8, torch.device("cuda"), dtype=torch.bfloat16, compute_dtype=torch.bfloat16)
+    # reference test_rdna3.py:713-723: rank 343 is FP16 only
+    from rdna3_fastmm.runtime import Rank343Plan
+
+    with pytest.raises(ValueError, match="does not support"):
+        Rank343Plan(8, 8, 8, torch.device("cuda"), dtype=torch.bfloat16, compute_dtype=torch.float16)
+    assert Rank343Plan.rank == 343 and Rank343Plan.scheme_size == 8
     # rank 49 offers BF16 leaves like the reference (runtime.py:852-858); bytes follow compute_dtype
     bf16_leaves = Rank49Plan(5, 6, 7, torch.device("cuda"), dtype=torch.bfloat16, compute_dtype=torch.bfloat16)
     assert bf16_leaves.compute_dtype == torch.bfloat16
