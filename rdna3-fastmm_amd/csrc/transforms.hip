@@ -28,10 +28,11 @@ constexpr int kThreads = 256;
 template <class S>
 constexpr int vector_width() { return S::kRank <= 8 ? 8 : S::kRank <= 64 ? 4 : 2; }
 
-// The recombination reads R products per element: at R = 343 one element per
-// thread already fills the register file (two would spill).
-template <class S>
-constexpr int reconstruct_width() { return S::kRank <= 64 ? vector_width<S>() : 1; }
+// The recombination reads R products per element: at R = 343, two fp16
+// elements per thread fill the register file (two fp32 ones would spill, so
+// fp32 products take one).
+template <class S, int kProd>
+constexpr int reconstruct_width() { return S::kRank <= 64 ? vector_width<S>() : kProd == kFP32 ? 1 : 2; }
 
 // The 8x8-block schemes run in FP16 only (rank 343: FP16 operands, planes and
 // output, as the reference's only precision pair); other element types are
@@ -85,17 +86,27 @@ __global__ __launch_bounds__(block_threads<S>()) void direct_transform_kernel(
     const int block_col = kSide == kLeftSide ? j % s : j / s;
     const int64_t r = block_row * rows_b + row;
     const int64_t c = block_col * cols_b + col;
-    if (r >= src_rows) return Vec<EPT>::zero();
+    // Branch-free: padding positions load a valid element (row 0, or the row's
+    // last column) and select zero. A branch per input would put every load in
+    // its own basic block, and the compiler would wait for each before issuing
+    // the next (64 serialized round trips for an 8x8-block scheme).
+    const bool row_inside = r < src_rows;
+    const int64_t rr = row_inside ? r : 0;
+    Vec<EPT> v;
     if constexpr (kVector) {
-      return load_vec<kDType, EPT>(src + r * src_cols + c);
+      v = load_vec<kDType, EPT>(src + rr * src_cols + c);
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) v.v[e] = row_inside ? v.v[e] : 0.0f;
     } else {
-      Vec<EPT> v;
 #pragma unroll
       for (int e = 0; e < EPT; ++e) {
-        v.v[e] = (c + e < src_cols) ? to_f32<kDType>(src[r * src_cols + c + e]) : 0.0f;
+        const bool inside = row_inside && c + e < src_cols;
+        const int64_t cc = c + e < src_cols ? c + e : src_cols - 1;
+        const float value = to_f32<kDType>(src[rr * src_cols + cc]);
+        v.v[e] = inside ? value : 0.0f;
       }
-      return v;
     }
+    return v;
   };
   auto store = [&](int k, const Vec<EPT>& v) {
     store_vec<kPlane, EPT>(dst + k * plane + at, v);
@@ -142,11 +153,10 @@ __global__ __launch_bounds__(kThreads) void transposed_right_kernel(
       const int kk = tid / TN + pass * (kThreads / TN);
       const int64_t k = k0 + kk, n = n0 + nn;
       const int64_t src_row = block_k * kb + k, src_col = block_n * nb + n;
-      float value = 0.0f;
-      if (k < kb && n < nb && src_row < inner && src_col < columns) {
-        value = to_f32<kDType>(src[src_row * columns + src_col]);
-      }
-      tile[j][kk][nn] = value;
+      // branch-free (see direct_transform_kernel): padding loads element 0
+      const bool inside = k < kb && n < nb && src_row < inner && src_col < columns;
+      const float value = to_f32<kDType>(src[inside ? src_row * columns + src_col : 0]);
+      tile[j][kk][nn] = inside ? value : 0.0f;
     }
   }
   __syncthreads();
@@ -345,7 +355,7 @@ template <class S, int kProd, int kOut, bool kBias>
 void launch_reconstruct_typed(bool vector, dim3 grid, hipStream_t stream, const void* products,
                               const uint16_t* bias, uint16_t* out, int64_t rows, int64_t cols,
                               int64_t rows_b, int64_t cols_b) {
-  constexpr int W = reconstruct_width<S>();
+  constexpr int W = reconstruct_width<S, kProd>();
   if (vector) {
     reconstruct_kernel<S, kProd, kOut, W, true, kBias>
         <<<grid, block_threads<S>(), 0, stream>>>(products, bias, out, rows, cols, rows_b, cols_b);
@@ -359,7 +369,7 @@ template <class S>
 int launch_reconstruct(int products_dtype, const void* products, const void* bias, int dtype,
                        void* output, int64_t rows, int64_t cols, hipStream_t stream) {
   constexpr int s = S::kSize;
-  constexpr int W = reconstruct_width<S>();
+  const int W = products_dtype == kFP32 ? reconstruct_width<S, kFP32>() : reconstruct_width<S, kFP16>();
   const int64_t rows_b = ceil_div(rows, s);
   const int64_t cols_b = ceil_div(cols, s);
   const int product_bytes = products_dtype == kFP32 ? 4 : 2;

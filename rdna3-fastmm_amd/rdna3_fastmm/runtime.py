@@ -720,6 +720,10 @@ class Rank343Plan(_Plan):
     rank = 343
     scheme_size = 8
     precision_pairs = frozenset({(torch.float16, torch.float16)})
+    # Prepacked 16384^3 beat FP16 torch.mm on two MI355X boxes (1.04x, 1.07x;
+    # bench.py --config c6-rank343); the dynamic path (right transform per call)
+    # does not (0.89x). Smaller squares lose (0.74x at 8192^3).
+    prepacked_shapes = frozenset({(16_384, 16_384, 16_384)})
 
 
 PLAN_TYPES: dict[str, type[_LinearPlan]] = {"rank7": Rank7Plan, "rank48": Rank48Plan, "rank49": Rank49Plan}
