@@ -256,6 +256,7 @@ def main() -> int:
             workspace.left_transformed,
             packed.transformed if packed is not None else workspace.right_transformed,
             workspace.products,
+            workspace.leaf_scratch,
         ),
         "reconstruct": lambda: plan._reconstruct(workspace.products, b, native_out),
     }

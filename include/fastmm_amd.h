@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define FASTMM_ABI_VERSION 4
+#define FASTMM_ABI_VERSION 5
 
 #define FASTMM_OK 0
 #define FASTMM_ERROR_ARGUMENT 1    /* bad pointer, size, dtype or scheme */
@@ -99,11 +99,25 @@ int fastmm_right_transform(int scheme, int dtype, int plane_dtype, const void* r
  * (operand_dtype = the planes' type) with fp32 accumulation, stored as
  * products_dtype: operand_dtype (the reference's torch.bmm rounding) or
  * FASTMM_FP32 (no product rounding).
- * Replaces torch.bmm(A', B', out=P) (runtime.py:728-732, 768-772). */
+ * Replaces torch.bmm(A', B', out=P) (runtime.py:728-732, 768-772).
+ *
+ * scratch / scratch_bytes: caller-owned device memory (16-byte aligned) for
+ * the split-K tail, at least fastmm_leaf_scratch_bytes() for the same
+ * arguments on the current device, or NULL / 0. With it, the last partial
+ * round of 256x256 tiles is split along K over the idle compute units and
+ * its fp32 parts are added in K order before the one products rounding;
+ * without it the tail runs as whole tiles (same results up to fp32 summation
+ * order). Calls that share one scratch buffer must not overlap. */
 int fastmm_leaf_products(int rank, int operand_dtype, const void* left_transformed,
                          const void* right_transformed, void* products, int products_dtype,
                          int64_t block_rows, int64_t block_inner, int64_t block_columns,
-                         void* stream);
+                         void* scratch, int64_t scratch_bytes, void* stream);
+
+/* Scratch bytes fastmm_leaf_products can use for these arguments on the
+ * current device (0 when the shape runs no split-K tail). No counterpart in
+ * the reference (torch.bmm manages its own workspace). */
+int fastmm_leaf_scratch_bytes(int rank, int operand_dtype, int products_dtype, int64_t block_rows,
+                              int64_t block_inner, int64_t block_columns, int64_t* bytes);
 
 /* Output recombination P[R, Mb, Nb] (products_dtype: fp16, bf16 or fp32) ->
  * output[rows, columns] in dtype, with an optional bias[columns] (NULL = none)

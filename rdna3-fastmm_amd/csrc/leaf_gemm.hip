@@ -39,6 +39,8 @@
 // Generic kernel (any Kb, any alignment): 256 x 256 tile, BK = 64, register-
 // staged loads with zero fill, double-buffered LDS; used for small or ragged
 // shapes where the fast kernel's preconditions fail.
+#include <algorithm>
+
 #include "abi_common.h"
 #include "fastmm_device.h"
 
@@ -47,19 +49,10 @@ namespace fastmm {
 constexpr int kGemmThreads = 256;
 constexpr int kTile = 256;
 
-// Workgroups are dispatched round-robin over the 8 XCDs (workgroup w runs on
-// XCD w % 8); renumber so that each XCD works on a contiguous range of tiles
-// (tiles of one leaf share A'/B' rows in that XCD's L2): with q = total / 8
-// and r = total % 8, XCD x receives q + 1 workgroups if x < r, else q, and
-// takes the logical tiles starting at x*(q+1) (x < r) or r*(q+1) + (x-r)*q.
-// Then walk the tiles of a leaf in groups of `group` tile rows, column by
-// column.
-__device__ __forceinline__ void decode_tile(int wg, int total, int tiles_m, int tiles_n,
-                                            int group, int& leaf, int& tm, int& tn) {
-  constexpr int kXcds = 8;
-  const int q = total / kXcds, r = total - q * kXcds;
-  const int x = wg % kXcds, i = wg / kXcds;
-  const int logical = x < r ? x * (q + 1) + i : r * (q + 1) + (x - r) * q + i;
+// Logical tile -> (leaf, tile row, tile column): walk the tiles of a leaf in
+// groups of `group` tile rows, column by column.
+__device__ __forceinline__ void tile_of(int logical, int tiles_m, int tiles_n, int group, int& leaf, int& tm,
+                                        int& tn) {
   const int per_leaf = tiles_m * tiles_n;
   leaf = logical / per_leaf;
   const int t = logical - leaf * per_leaf;
@@ -69,6 +62,19 @@ __device__ __forceinline__ void decode_tile(int wg, int total, int tiles_m, int 
   const int within = t - g * group * tiles_n;
   tm = first_m + within % rows_in_group;
   tn = within / rows_in_group;
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup w runs on
+// XCD w % 8); renumber so that each XCD works on a contiguous range of tiles
+// (tiles of one leaf share A'/B' rows in that XCD's L2): with q = total / 8
+// and r = total % 8, XCD x receives q + 1 workgroups if x < r, else q, and
+// takes the logical tiles starting at x*(q+1) (x < r) or r*(q+1) + (x-r)*q.
+__device__ __forceinline__ void decode_tile(int wg, int total, int tiles_m, int tiles_n,
+                                            int group, int& leaf, int& tm, int& tn) {
+  constexpr int kXcds = 8;
+  const int q = total / kXcds, r = total - q * kXcds;
+  const int x = wg % kXcds, i = wg / kXcds;
+  tile_of(x < r ? x * (q + 1) + i : r * (q + 1) + (x - r) * q + i, tiles_m, tiles_n, group, leaf, tm, tn);
 }
 
 // 32x32x16 MFMA on 8 operand elements per lane, fp16 or bf16 (same register
@@ -349,14 +355,32 @@ using Int = std::integral_constant<int, V>;
 template <bool V>
 using Bool = std::integral_constant<bool, V>;
 
-template <int kIn, int kOut>
+// kPartial (the split-K tail of a launch): workgroup w computes K part
+// w / tail_count (of `split` contiguous runs of whole 4-slice groups) of
+// logical tile tail_base + w % tail_count, and stores the unmasked 256 x 256
+// fp32 partial sum at partial + (tile * split + part) * 256 * 256 (row-major);
+// tail_reduce_kernel adds the parts. Otherwise workgroup w computes the whole
+// K range of one of the first total_tiles logical tiles (XCD order).
+template <int kIn, int kOut, bool kPartial>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B,
                       void* __restrict__ P, int Mb, int Nb, int Kb, int tiles_m, int tiles_n,
-                      int total_tiles) {
+                      int total_tiles, int tail_base, int tail_count, int split) {
   extern __shared__ __attribute__((aligned(16))) half_t smem[];
   int leaf, tm, tn;
-  decode_tile(blockIdx.x, total_tiles, tiles_m, tiles_n, 8, leaf, tm, tn);
+  int k_first = 0, nk = Kb / BK;  // slices; nk is a multiple of 4, checked by the launcher
+  int tile_slot = 0;
+  if constexpr (kPartial) {
+    const int t = blockIdx.x % tail_count, part = blockIdx.x / tail_count;
+    tile_of(tail_base + t, tiles_m, tiles_n, 8, leaf, tm, tn);
+    const int groups = nk / 4;
+    const int g0 = part * groups / split, g1 = (part + 1) * groups / split;
+    k_first = 4 * g0;
+    nk = 4 * (g1 - g0);
+    tile_slot = t * split + part;
+  } else {
+    decode_tile(blockIdx.x, total_tiles, tiles_m, tiles_n, 8, leaf, tm, tn);
+  }
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
@@ -427,7 +451,7 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
     half_t* dst = smem + slot * STAGE_HALVES + (b_side ? kTile * BK : 0) + (q * 4 + wave) * 16 * BK;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(b_side ? b_rsrc : a_rsrc, (lds_ptr)(dst), 16,
                                              b_side ? b_off[q] : a_off[q],
-                                             kt * (b_side ? Nb : Mb) * kSlab * 2, 0, 0);
+                                             (k_first + kt) * (b_side ? Nb : Mb) * kSlab * 2, 0, 0);
   };
 #define FASTMM_READ(kSlotSrc, kSet, r)                                                              \
   do {                                                                                              \
@@ -497,7 +521,6 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
     if constexpr (kSync) fast::barrier();
   };
 
-  const int nk = Kb / BK;  // multiple of 4, checked by the launcher
 #pragma unroll
   for (int s = 0; s < STAGES; ++s)
 #pragma unroll
@@ -542,7 +565,17 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
   int lane_now;
   asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane_now));
   const int out_row = wm * 128 + (lane_now & 15), out_col = wn * 128 + 4 * (lane_now >> 4);
-  if constexpr (kOut == kFP32) {
+  if constexpr (kPartial) {
+    float* tile_at = static_cast<float*>(P) + static_cast<int64_t>(tile_slot) * kTile * kTile;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        *reinterpret_cast<float4*>(tile_at + (out_row + i * 16) * kTile + out_col + j * 16) =
+            make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+      }
+    }
+  } else if constexpr (kOut == kFP32) {
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       const int row = m0 + out_row + i * 16;
@@ -719,6 +752,78 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
 
 }  // namespace generic
 
+// ------------------------------------------------------------- split-K tail
+
+// Sum of the `split` fp32 parts of each tail tile, in K order, cast to the
+// products type and stored inside the leaf (rows < Mb, columns < Nb). A thread
+// owns 4 consecutive columns of one tile row; Nb % 4 == 0 (checked by the
+// launcher), so the 4 are all inside or all outside.
+template <int kOut>
+__global__ __launch_bounds__(256) void tail_reduce_kernel(const float* __restrict__ partial, void* __restrict__ P,
+                                                          int Mb, int Nb, int tiles_m, int tiles_n, int tail_base,
+                                                          int split) {
+  const int t = blockIdx.y;
+  const int e = (blockIdx.x * 256 + threadIdx.x) * 4;
+  int leaf, tm, tn;
+  tile_of(tail_base + t, tiles_m, tiles_n, 8, leaf, tm, tn);
+  const int row = tm * kTile + (e / kTile), col = tn * kTile + (e % kTile);
+  if (row >= Mb || col >= Nb) return;
+  const float* part = partial + static_cast<int64_t>(t) * split * kTile * kTile + e;
+  float4 sum = *reinterpret_cast<const float4*>(part);
+  for (int p = 1; p < split; ++p) {
+    const float4 v = *reinterpret_cast<const float4*>(part + static_cast<int64_t>(p) * kTile * kTile);
+    sum.x += v.x;
+    sum.y += v.y;
+    sum.z += v.z;
+    sum.w += v.w;
+  }
+  const int64_t at = static_cast<int64_t>(leaf) * Mb * Nb + static_cast<int64_t>(row) * Nb + col;
+  if constexpr (kOut == kFP32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(P) + at) = sum;
+  } else {
+    uint16_t h[4] = {from_f32<kOut>(sum.x), from_f32<kOut>(sum.y), from_f32<kOut>(sum.z), from_f32<kOut>(sum.w)};
+    store16<4>(static_cast<uint16_t*>(P) + at, h);
+  }
+}
+
+// Compute units of the current device (cached per device; 0 if unknown).
+int compute_units() {
+  static int cached[64] = {};
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 0;
+  if (cached[device] == 0) {
+    int units = 0;
+    if (hipDeviceGetAttribute(&units, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return 0;
+    cached[device] = units;
+  }
+  return cached[device];
+}
+
+// One workgroup per CU: `total` tiles run in ceil(total / CUs) rounds, and a
+// last round of `tail` < CUs tiles leaves CUs idle for a whole tile time. When
+// the tail fills at most half the CUs, its tiles are split along K into
+// `split` = min(4, CUs / tail, groups of 4 slices) parts run side by side,
+// then added by tail_reduce_kernel: the last round takes ~1/split of a tile
+// time plus the reduction.
+struct TailSplit {
+  int64_t main_tiles, tail, split;
+};
+
+TailSplit tail_split(int64_t total, int64_t kb) {
+  const int64_t cus = compute_units();
+  const int64_t groups = kb / (4 * mfma16::BK);
+  if (cus <= 0) return {total, 0, 1};
+  const int64_t tail = total % cus;
+  if (tail == 0) return {total, 0, 1};
+  const int64_t split = std::min<int64_t>({4, cus / tail, groups});
+  if (split < 2) return {total, 0, 1};
+  return {total - tail, tail, split};
+}
+
+int64_t tail_scratch_bytes(const TailSplit& plan) {
+  return plan.tail * plan.split * kTile * kTile * static_cast<int64_t>(sizeof(float));
+}
+
 // ---------------------------------------------------------------- launchers
 
 template <class Kernel>
@@ -759,6 +864,56 @@ bool mfma16_leaf_gemm_applies(int64_t mb, int64_t kb, int64_t nb) {
          (nb + kTile) * kb * 2 <= INT32_MAX;
 }
 
+template <class Kernel>
+int reserve_lds(Kernel kernel, int lds_bytes, bool& configured) {
+  if (!configured) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            lds_bytes) != hipSuccess) {
+      return fail(FASTMM_ERROR_LAUNCH, "leaf products: cannot reserve %d bytes of LDS", lds_bytes);
+    }
+    configured = true;
+  }
+  return FASTMM_OK;
+}
+
+// The 16x16x32 kernel over all tiles, with the split-K tail when scratch
+// holds its partial sums (otherwise the tail runs as whole tiles).
+template <int kIn, int kOut>
+int launch_mfma16(const void* a, const void* b, void* p, int64_t rank, int64_t mb, int64_t kb, int64_t nb,
+                  void* scratch, int64_t scratch_bytes, hipStream_t stream) {
+  static bool main_ready = false, partial_ready = false;
+  auto* main_kernel = mfma16::leaf_gemm_kernel<kIn, kOut, false>;
+  auto* partial_kernel = mfma16::leaf_gemm_kernel<kIn, kFP32, true>;
+  if (int status = reserve_lds(main_kernel, mfma16::LDS_BYTES, main_ready)) return status;
+  if (int status = reserve_lds(partial_kernel, mfma16::LDS_BYTES, partial_ready)) return status;
+  const int64_t tiles_m = ceil_div(mb, kTile), tiles_n = ceil_div(nb, kTile);
+  const int64_t total = tiles_m * tiles_n * rank;
+  if (total > INT32_MAX / 4) return fail(FASTMM_ERROR_UNSUPPORTED, "leaf products: too many tiles");
+  TailSplit plan = tail_split(total, kb);
+  if (plan.tail > 0 && (scratch == nullptr || scratch_bytes < tail_scratch_bytes(plan) ||
+                        !aligned_to(scratch, 16))) {
+    plan = {total, 0, 1};
+  }
+  const half_t* A = static_cast<const half_t*>(a);
+  const half_t* B = static_cast<const half_t*>(b);
+  const int M = static_cast<int>(mb), N = static_cast<int>(nb), K = static_cast<int>(kb);
+  const int TM = static_cast<int>(tiles_m), TN = static_cast<int>(tiles_n);
+  if (plan.main_tiles > 0) {
+    main_kernel<<<dim3(static_cast<unsigned>(plan.main_tiles)), kGemmThreads, mfma16::LDS_BYTES, stream>>>(
+        A, B, p, M, N, K, TM, TN, static_cast<int>(plan.main_tiles), 0, 1, 1);
+    if (int status = check_launch("leaf products")) return status;
+  }
+  if (plan.tail == 0) return FASTMM_OK;
+  const int tail = static_cast<int>(plan.tail), split = static_cast<int>(plan.split);
+  const int base = static_cast<int>(plan.main_tiles);
+  partial_kernel<<<dim3(static_cast<unsigned>(tail * split)), kGemmThreads, mfma16::LDS_BYTES, stream>>>(
+      A, B, scratch, M, N, K, TM, TN, 0, base, tail, split);
+  if (int status = check_launch("leaf products (split-K tail)")) return status;
+  tail_reduce_kernel<kOut><<<dim3(kTile * kTile / 4 / 256, static_cast<unsigned>(tail)), 256, 0, stream>>>(
+      static_cast<const float*>(scratch), p, M, N, TM, TN, base, split);
+  return check_launch("leaf products (tail reduction)");
+}
+
 }  // namespace fastmm
 
 using namespace fastmm;
@@ -768,9 +923,9 @@ namespace fastmm {
 // Kernel choice for one (operand, products) element-type pair.
 template <int kIn, int kOut>
 int launch_leaf_products(const void* a, const void* b, void* p, int64_t rank, int64_t mb, int64_t kb,
-                         int64_t nb, hipStream_t s) {
+                         int64_t nb, void* scratch, int64_t scratch_bytes, hipStream_t s) {
   if (fast_leaf_gemm_applies(a, b, p, kb, nb, kOut) && mfma16_leaf_gemm_applies(mb, kb, nb)) {
-    return launch_tiles(mfma16::leaf_gemm_kernel<kIn, kOut>, mfma16::LDS_BYTES, a, b, p, rank, mb, kb, nb, s);
+    return launch_mfma16<kIn, kOut>(a, b, p, rank, mb, kb, nb, scratch, scratch_bytes, s);
   }
   if (fast_leaf_gemm_applies(a, b, p, kb, nb, kOut)) {
     return launch_tiles(fast::leaf_gemm_kernel<kIn, kOut>, fast::LDS_BYTES, a, b, p, rank, mb, kb, nb, s);
@@ -797,8 +952,13 @@ int launch_leaf_products(const void* a, const void* b, void* p, int64_t rank, in
 extern "C" int fastmm_leaf_products(int rank, int operand_dtype, const void* left_transformed,
                                     const void* right_transformed, void* products,
                                     int products_dtype, int64_t block_rows, int64_t block_inner,
-                                    int64_t block_columns, void* stream) {
+                                    int64_t block_columns, void* scratch, int64_t scratch_bytes,
+                                    void* stream) {
   clear_error();
+  if (scratch_bytes < 0 || (scratch == nullptr && scratch_bytes != 0)) {
+    return fail(FASTMM_ERROR_ARGUMENT, "leaf products: scratch of %lld bytes at null",
+                static_cast<long long>(scratch_bytes));
+  }
   if (left_transformed == nullptr || right_transformed == nullptr || products == nullptr) {
     return fail(FASTMM_ERROR_ARGUMENT, "leaf products: null pointer");
   }
@@ -822,10 +982,36 @@ extern "C" int fastmm_leaf_products(int rank, int operand_dtype, const void* lef
   const void* b = right_transformed;
   void* p = products;
   const int64_t mb = block_rows, kb = block_inner, nb = block_columns;
+  void* w = scratch;
+  const int64_t wb = scratch_bytes;
   if (operand_dtype == kBF16) {
-    if (products_dtype == kFP32) return launch_leaf_products<kBF16, kFP32>(a, b, p, rank, mb, kb, nb, s);
-    return launch_leaf_products<kBF16, kBF16>(a, b, p, rank, mb, kb, nb, s);
+    if (products_dtype == kFP32) return launch_leaf_products<kBF16, kFP32>(a, b, p, rank, mb, kb, nb, w, wb, s);
+    return launch_leaf_products<kBF16, kBF16>(a, b, p, rank, mb, kb, nb, w, wb, s);
   }
-  if (products_dtype == kFP32) return launch_leaf_products<kFP16, kFP32>(a, b, p, rank, mb, kb, nb, s);
-  return launch_leaf_products<kFP16, kFP16>(a, b, p, rank, mb, kb, nb, s);
+  if (products_dtype == kFP32) return launch_leaf_products<kFP16, kFP32>(a, b, p, rank, mb, kb, nb, w, wb, s);
+  return launch_leaf_products<kFP16, kFP16>(a, b, p, rank, mb, kb, nb, w, wb, s);
+}
+
+extern "C" int fastmm_leaf_scratch_bytes(int rank, int operand_dtype, int products_dtype, int64_t block_rows,
+                                         int64_t block_inner, int64_t block_columns, int64_t* bytes) {
+  clear_error();
+  if (bytes == nullptr) return fail(FASTMM_ERROR_ARGUMENT, "leaf scratch bytes: null result pointer");
+  *bytes = 0;
+  if (rank < 1 || block_rows < 1 || block_inner < 1 || block_columns < 1) {
+    return fail(FASTMM_ERROR_ARGUMENT, "leaf scratch bytes: dimensions must be positive");
+  }
+  if ((operand_dtype != kFP16 && operand_dtype != kBF16) ||
+      (products_dtype != operand_dtype && products_dtype != kFP32)) {
+    return fail(FASTMM_ERROR_ARGUMENT, "leaf scratch bytes: unsupported element types %d -> %d", operand_dtype,
+                products_dtype);
+  }
+  // the split-K tail runs on the 16x16x32 path (16-byte aligned buffers assumed)
+  const int64_t out_align = products_dtype == kFP32 ? 4 : 8;
+  if (block_inner % fast::BK != 0 || block_inner < 3 * fast::BK || block_columns % out_align != 0 ||
+      !mfma16_leaf_gemm_applies(block_rows, block_inner, block_columns)) {
+    return FASTMM_OK;
+  }
+  const int64_t total = ceil_div(block_rows, kTile) * ceil_div(block_columns, kTile) * rank;
+  *bytes = tail_scratch_bytes(tail_split(total, block_inner));
+  return FASTMM_OK;
 }

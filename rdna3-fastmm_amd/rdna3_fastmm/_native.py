@@ -15,7 +15,7 @@ import torch
 
 from ._build import LIBRARY_PATH
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 BF16, FP16, FP32 = 0, 1, 2
 _DTYPE_CODES = {torch.bfloat16: BF16, torch.float16: FP16, torch.float32: FP32}
@@ -29,7 +29,8 @@ SIGNATURES: dict[str, list] = {
     "fastmm_left_transform": [_INT, _INT, _INT, _PTR, _PTR, _I64, _I64, _PTR],
     "fastmm_weight_transform": [_INT, _INT, _INT, _PTR, _PTR, _I64, _I64, _PTR],
     "fastmm_right_transform": [_INT, _INT, _INT, _PTR, _PTR, _I64, _I64, _PTR],
-    "fastmm_leaf_products": [_INT, _INT, _PTR, _PTR, _PTR, _INT, _I64, _I64, _I64, _PTR],
+    "fastmm_leaf_products": [_INT, _INT, _PTR, _PTR, _PTR, _INT, _I64, _I64, _I64, _PTR, _I64, _PTR],
+    "fastmm_leaf_scratch_bytes": [_INT, _INT, _INT, _I64, _I64, _I64, ctypes.POINTER(_I64)],
     "fastmm_reconstruct": [_INT, _INT, _PTR, _PTR, _INT, _PTR, _I64, _I64, _PTR],
     "fastmm_scheme_info": [_INT, ctypes.POINTER(_INT), ctypes.POINTER(_INT)],
 }

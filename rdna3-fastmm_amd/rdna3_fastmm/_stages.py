@@ -8,6 +8,8 @@ and leaf operands in the plan's compute dtype, products likewise (or fp32).
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _native
@@ -67,7 +69,9 @@ def leaf_products(
     block_rows: int,
     block_inner: int,
     block_columns: int,
+    scratch: torch.Tensor | None = None,
 ) -> None:
+    """``scratch`` (bytes on the same device, or None): the split-K tail's fp32 parts."""
     with torch.cuda.device(left.device):
         _native.call(
             "fastmm_leaf_products",
@@ -80,8 +84,35 @@ def leaf_products(
             block_rows,
             block_inner,
             block_columns,
+            None if scratch is None else scratch.data_ptr(),
+            0 if scratch is None else scratch.numel() * scratch.element_size(),
             _native.stream_handle(left.device),
         )
+
+
+def leaf_scratch_bytes(
+    rank: int,
+    operand_dtype: torch.dtype,
+    products_dtype: torch.dtype,
+    block_rows: int,
+    block_inner: int,
+    block_columns: int,
+    device: torch.device,
+) -> int:
+    """Scratch bytes the leaf products can use for this shape on ``device`` (0: none)."""
+    result = ctypes.c_int64(0)
+    with torch.cuda.device(device):
+        _native.call(
+            "fastmm_leaf_scratch_bytes",
+            rank,
+            _native.dtype_code(operand_dtype),
+            _native.dtype_code(products_dtype),
+            block_rows,
+            block_inner,
+            block_columns,
+            ctypes.byref(result),
+        )
+    return int(result.value)
 
 
 def reconstruct(

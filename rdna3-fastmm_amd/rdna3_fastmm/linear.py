@@ -73,8 +73,10 @@ def _linear(plan_type: type, name: str, input_tensor: torch.Tensor, weight: torc
     _stages.left_transform(scheme, flat, left, rows, inner)
     _stages.weight_transform(scheme, weight, right, columns, inner)
     products = torch.empty((rank, mb, nb), device=device, dtype=torch.float16)
-    _stages.leaf_products(rank, left, right, products, mb, kb, nb)
-    del left, right
+    scratch_bytes = _stages.leaf_scratch_bytes(rank, torch.float16, torch.float16, mb, kb, nb, device)
+    scratch = torch.empty(scratch_bytes, device=device, dtype=torch.uint8) if scratch_bytes else None
+    _stages.leaf_products(rank, left, right, products, mb, kb, nb, scratch)
+    del left, right, scratch
     output = torch.empty((rows, columns), device=device, dtype=input_tensor.dtype)
     _stages.reconstruct(scheme, products, bias, output, rows, columns)
     return output.reshape(*input_tensor.shape[:-1], columns)

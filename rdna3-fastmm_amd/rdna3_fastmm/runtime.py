@@ -99,6 +99,10 @@ class Workspace:
     left_transformed: torch.Tensor
     right_transformed: torch.Tensor | None
     products: torch.Tensor
+    # MI355X-specific: bytes for the leaf GEMM's split-K tail (None when the
+    # shape has none, or for a workspace built by hand: the tail then runs as
+    # whole tiles). Not part of the reference's byte formulas.
+    leaf_scratch: torch.Tensor | None = None
 
 
 @dataclass(frozen=True)
@@ -301,6 +305,15 @@ class _Plan:
         shape = self.shape
         return self.rank * shape.block_inner * shape.block_columns * self.compute_dtype.itemsize
 
+    @property
+    def leaf_scratch_bytes(self) -> int:
+        """Device bytes of ``Workspace.leaf_scratch`` (the leaf GEMM's split-K tail)."""
+        shape = self.shape
+        return _stages.leaf_scratch_bytes(
+            self.rank, self.compute_dtype, self.compute_dtype, shape.block_rows, shape.block_inner,
+            shape.block_columns, self.device,
+        )
+
     def _workspace_bytes(self, prepacked_right: bool) -> int:
         shape = self.shape
         elements = self.rank * (
@@ -324,8 +337,10 @@ class _Plan:
     def allocate_workspace(
         self, max_free_memory_fraction: float = 0.75, *, prepacked_right: bool = False
     ) -> Workspace:
+        scratch_bytes = self.leaf_scratch_bytes
         self._ensure_memory_budget(
-            self._workspace_bytes(prepacked_right), max_free_memory_fraction, f"{self.algorithm} workspace"
+            self._workspace_bytes(prepacked_right) + scratch_bytes, max_free_memory_fraction,
+            f"{self.algorithm} workspace",
         )
         shape = self.shape
         return Workspace(
@@ -337,6 +352,7 @@ class _Plan:
             if prepacked_right
             else self._empty(operand_shape(self.rank, shape.block_columns, shape.block_inner)),
             products=self._empty((self.rank, shape.block_rows, shape.block_columns)),
+            leaf_scratch=torch.empty(scratch_bytes, device=self.device, dtype=torch.uint8) if scratch_bytes else None,
         )
 
     def _empty(self, shape: tuple[int, ...]) -> torch.Tensor:
@@ -372,13 +388,14 @@ class _Plan:
         self._validate_workspace(workspace, require_right=True)
         result = self._output(output)
         self._validate_output_storage(
-            result, left, right, workspace.left_transformed, workspace.products, workspace.right_transformed
+            result, left, right, workspace.left_transformed, workspace.products, workspace.right_transformed,
+            workspace.leaf_scratch,
         )
         right_transformed = workspace.right_transformed
         assert right_transformed is not None
         self._transform_left(left, workspace.left_transformed)
         self._transform_right(right, right_transformed)
-        self._leaf_products(workspace.left_transformed, right_transformed, workspace.products)
+        self._leaf_products(workspace.left_transformed, right_transformed, workspace.products, workspace.leaf_scratch)
         self._reconstruct(workspace.products, None, result)
         return result
 
@@ -401,9 +418,10 @@ class _Plan:
             workspace.left_transformed,
             workspace.products,
             workspace.right_transformed,
+            workspace.leaf_scratch,
         )
         self._transform_left(left, workspace.left_transformed)
-        self._leaf_products(workspace.left_transformed, right.transformed, workspace.products)
+        self._leaf_products(workspace.left_transformed, right.transformed, workspace.products, workspace.leaf_scratch)
         self._reconstruct(workspace.products, None, result)
         return result
 
@@ -418,10 +436,12 @@ class _Plan:
     def _transform_weight(self, source: torch.Tensor, output: torch.Tensor) -> None:
         _stages.weight_transform(self.scheme, source, output, self.shape.columns, self.shape.inner)
 
-    def _leaf_products(self, left: torch.Tensor, right: torch.Tensor, products: torch.Tensor) -> None:
+    def _leaf_products(
+        self, left: torch.Tensor, right: torch.Tensor, products: torch.Tensor, scratch: torch.Tensor | None = None
+    ) -> None:
         shape = self.shape
         _stages.leaf_products(
-            self.rank, left, right, products, shape.block_rows, shape.block_inner, shape.block_columns
+            self.rank, left, right, products, shape.block_rows, shape.block_inner, shape.block_columns, scratch
         )
 
     def _reconstruct(self, products: torch.Tensor, bias: torch.Tensor | None, output: torch.Tensor) -> None:
@@ -478,7 +498,16 @@ class _Plan:
                 or tensor.requires_grad
             ):
                 raise ValueError("workspace does not match the plan")
-        self._validate_separate_storage(*(tensor for tensor, _ in expected))
+        scratch = workspace.leaf_scratch
+        if scratch is not None and (
+            scratch.device != self.device or scratch.dtype != torch.uint8 or scratch.dim() != 1
+            or not scratch.is_contiguous()
+        ):
+            raise ValueError("workspace does not match the plan")
+        tensors = [tensor for tensor, _ in expected]
+        if scratch is not None and scratch.numel():
+            tensors.append(scratch)
+        self._validate_separate_storage(*tensors)
 
     def _validate_packed_right(self, packed: PackedRight) -> None:
         if not isinstance(packed, PackedRight):
@@ -627,12 +656,13 @@ class _LinearPlan(_Plan):
             workspace.left_transformed,
             workspace.products,
             workspace.right_transformed,
+            workspace.leaf_scratch,
         )
         right_transformed = workspace.right_transformed
         assert right_transformed is not None
         self._transform_left(input_tensor, workspace.left_transformed)
         self._transform_weight(weight, right_transformed)
-        self._leaf_products(workspace.left_transformed, right_transformed, workspace.products)
+        self._leaf_products(workspace.left_transformed, right_transformed, workspace.products, workspace.leaf_scratch)
         self._reconstruct(workspace.products, bias, result)
         return result
 
@@ -659,9 +689,10 @@ class _LinearPlan(_Plan):
             workspace.left_transformed,
             workspace.products,
             workspace.right_transformed,
+            workspace.leaf_scratch,
         )
         self._transform_left(input_tensor, workspace.left_transformed)
-        self._leaf_products(workspace.left_transformed, weight.transformed, workspace.products)
+        self._leaf_products(workspace.left_transformed, weight.transformed, workspace.products, workspace.leaf_scratch)
         self._reconstruct(workspace.products, bias, result)
         return result
 

@@ -147,6 +147,8 @@ def test_reconstruct_bit_exact(key, shape, product_dtype) -> None:
         # narrow columns, many leaves
         (7, 2048, 2304, 256), (2, 4107, 2304, 384), (48, 520, 512, 256), (17, 4000, 40, 256),
         (49, 1024, 1024, 512),
+        # split-K tail (with scratch): one tile in 4 K parts, ragged tiles, full rounds + a tail
+        (1, 256, 256, 1024), (2, 300, 520, 1024), (3, 2560, 2560, 256),
     ),
 )
 @pytest.mark.parametrize(
@@ -169,16 +171,24 @@ def test_leaf_products_within_fp32_accumulation_bound(dims, operand_dtype, produ
     a_dev = torch.from_numpy(to_operand(a.view(torch.int16).numpy())).to(DEVICE).view(operand_dtype)
     b_dev = torch.from_numpy(to_operand(b.view(torch.int16).numpy())).to(DEVICE).view(operand_dtype)
     _stages.leaf_products(rank, a_dev, b_dev, p, mb, kb, nb)
+    # the same launch with the split-K tail's scratch, and with a scratch too small to use
+    scratch_bytes = _stages.leaf_scratch_bytes(rank, operand_dtype, product_dtype, mb, kb, nb, DEVICE)
+    runs = [p]
+    for size in (scratch_bytes, 16) if scratch_bytes else ():
+        scratch = torch.empty(size, device=DEVICE, dtype=torch.uint8)
+        runs.append(torch.empty_like(p))
+        _stages.leaf_products(rank, a_dev, b_dev, runs[-1], mb, kb, nb, scratch)
+    print(f"[case] scratch bytes {scratch_bytes}", flush=True)
     torch.cuda.synchronize()
     a32, b32 = a.float().numpy(), b.float().numpy()
     exact = O.leaf_products(a32, b32, product_dtype="fp32")
     magnitude = np.matmul(np.abs(a32.astype(np.float64)), np.abs(np.swapaxes(b32.astype(np.float64), 1, 2)))
     bound = kb * 2.0**-24 * magnitude + 1e-30
-    got = p.float().cpu().numpy().astype(np.float64)
     if product_dtype == torch.float16:
         # one fp16 rounding of a value within `bound` of the exact sum
         bound = bound + np.abs(exact.astype(np.float64)) * 2.0**-11 + 2.0**-24
     if product_dtype == torch.bfloat16:
         # one bf16 rounding (8-bit significand)
         bound = bound + np.abs(exact.astype(np.float64)) * 2.0**-8 + 2.0**-126
-    assert np.all(np.abs(got - exact) <= bound)
+    for got in runs:
+        assert np.all(np.abs(got.float().cpu().numpy().astype(np.float64) - exact) <= bound)

@@ -25,6 +25,7 @@ def test_header_declares_the_stage_entry_points() -> None:
         "fastmm_weight_transform",
         "fastmm_right_transform",
         "fastmm_leaf_products",
+        "fastmm_leaf_scratch_bytes",
         "fastmm_reconstruct",
         "fastmm_abi_version",
         "fastmm_last_error",
@@ -61,11 +62,18 @@ def test_compiled_scheme_digests_match_verified_certificates() -> None:
         (lambda lib: lib.fastmm_weight_transform(0, 0, 7, 16, 16, 4, 4, None), b"planes must be fp16 or bf16"),
         (lambda lib: lib.fastmm_right_transform(1, 1, 1, 16, 16, 4, -1, None), b"positive"),
         (lambda lib: lib.fastmm_right_transform(1, 1, 2, 16, 16, 4, 4, None), b"planes must be fp16 or bf16"),
-        (lambda lib: lib.fastmm_leaf_products(7, 2, 16, 16, 16, 2, 2, 2, 2, None), b"operands must be fp16 or bf16"),
-        (lambda lib: lib.fastmm_leaf_products(7, 1, 16, 16, 16, 0, 2, 2, 2, None), b"products must be fp32 or"),
-        (lambda lib: lib.fastmm_leaf_products(7, 0, 16, 16, 16, 1, 2, 2, 2, None), b"products must be fp32 or"),
-        (lambda lib: lib.fastmm_leaf_products(0, 1, 16, 16, 16, 1, 2, 2, 2, None), b"positive"),
-        (lambda lib: lib.fastmm_leaf_products(7, 1, 16, 16, 16, 1, 1 << 20, 1 << 12, 2, None), b"2^31"),
+        (lambda lib: lib.fastmm_leaf_products(7, 2, 16, 16, 16, 2, 2, 2, 2, None, 0, None),
+         b"operands must be fp16 or bf16"),
+        (lambda lib: lib.fastmm_leaf_products(7, 1, 16, 16, 16, 0, 2, 2, 2, None, 0, None), b"products must be fp32 or"),
+        (lambda lib: lib.fastmm_leaf_products(7, 0, 16, 16, 16, 1, 2, 2, 2, None, 0, None), b"products must be fp32 or"),
+        (lambda lib: lib.fastmm_leaf_products(0, 1, 16, 16, 16, 1, 2, 2, 2, None, 0, None), b"positive"),
+        (lambda lib: lib.fastmm_leaf_products(7, 1, 16, 16, 16, 1, 1 << 20, 1 << 12, 2, None, 0, None), b"2^31"),
+        (lambda lib: lib.fastmm_leaf_products(7, 1, 16, 16, 16, 1, 2, 2, 2, None, 64, None), b"scratch of 64 bytes"),
+        (lambda lib: lib.fastmm_leaf_products(7, 1, 16, 16, 16, 1, 2, 2, 2, 16, -1, None), b"scratch of -1 bytes"),
+        (lambda lib: lib.fastmm_leaf_scratch_bytes(7, 1, 1, 2, 2, 2, None), b"null result pointer"),
+        (lambda lib: lib.fastmm_leaf_scratch_bytes(7, 2, 2, 2, 2, 2, ctypes.byref(ctypes.c_int64())),
+         b"unsupported element types"),
+        (lambda lib: lib.fastmm_leaf_scratch_bytes(7, 1, 1, 0, 2, 2, ctypes.byref(ctypes.c_int64())), b"positive"),
         (lambda lib: lib.fastmm_reconstruct(0, 3, 16, None, 0, 16, 4, 4, None), b"fp16, bf16 or fp32"),
         (lambda lib: lib.fastmm_reconstruct(9, 1, 16, None, 0, 16, 4, 4, None), b"unknown scheme"),
     ),
@@ -74,6 +82,17 @@ def test_argument_errors_are_reported_before_any_launch(call, message) -> None:
     lib = _native.library()
     assert call(lib) != 0
     assert message in lib.fastmm_last_error()
+
+
+def test_leaf_scratch_query_without_a_device_reports_no_tail() -> None:
+    """No GPU here: the query cannot see compute units and asks for no scratch;
+    shapes off the 16x16x32 path never need any."""
+    lib = _native.library()
+    size = ctypes.c_int64(-1)
+    assert lib.fastmm_leaf_scratch_bytes(7, 1, 1, 4107, 6144, 2304, ctypes.byref(size)) == 0
+    assert size.value == 0
+    assert lib.fastmm_leaf_scratch_bytes(7, 1, 1, 4107, 6150, 2304, ctypes.byref(size)) == 0
+    assert size.value == 0
 
 
 def test_missing_library_fails_loudly(tmp_path: Path) -> None:

@@ -136,9 +136,17 @@ def test_byte_formulas_and_precision_pairs(monkeypatch) -> None:
 def test_memory_budget_is_checked_before_allocation(monkeypatch) -> None:
     configure_supported_runtime(monkeypatch)
     monkeypatch.setattr(torch.cuda, "mem_get_info", lambda device=None: (1 << 28, 1 << 38))
+    scratch = {"bytes": 0}
+    monkeypatch.setattr(runtime._stages, "leaf_scratch_bytes", lambda *args: scratch["bytes"])
     plan = Rank7Plan(8192, 8192, 8192, torch.device("cuda"), dtype=torch.bfloat16, compute_dtype=torch.float16)
     with pytest.raises(MemoryError, match="budget"):
         plan.allocate_workspace()
+    # the leaf GEMM's split-K scratch counts against the same budget
+    small = Rank7Plan(256, 256, 256, torch.device("cuda"), dtype=torch.bfloat16, compute_dtype=torch.float16)
+    scratch["bytes"] = 1 << 28
+    assert small.leaf_scratch_bytes == 1 << 28
+    with pytest.raises(MemoryError, match="budget"):
+        small.allocate_workspace()
     with pytest.raises(ValueError, match="interval"):
         plan.allocate_workspace(max_free_memory_fraction=0)
 
