@@ -172,3 +172,10 @@ def test_sweep_families_group_by_scheme_mode_and_pair() -> None:
     assert document["families"] == combined and document["minimum_speedup"] == 1.0
     case = C.sweep_case(12288, 4608, True, 480)
     assert case.shape == (480, 12288, 4608) and case.bias and case.compute_dtype == "float16"
+
+
+def test_llm_corpus_loads() -> None:
+    corpus = C.load_corpus(C.DEFAULT_CORPUS_PATH.parent / "llm-mlp-2025.json")
+    assert len(corpus.cases) == 24 and all(not case.bias for case in corpus.cases)
+    down = corpus.case("llama-3-8b-4096-down")
+    assert down.shape == (4096, 14336, 4096) and down.projection == "MLP down projection"
