@@ -336,7 +336,9 @@ def main() -> int:
         "stages_ms": {name: round(v, 4) for name, v in stage_ms.items()},
         "packing_ms": round(pack_ms, 4),
         "roofline": {
-            "kernel": leaf_kernel_name(shape.block_inner, "bf16" if compute == torch.bfloat16 else "fp16"),
+            "kernel": leaf_kernel_name(shape.block_inner, "bf16" if compute == torch.bfloat16 else "fp16")
+            + (" + split-K tail (kPartial parts + tail_reduce_kernel); timed as the whole stage"
+               if workspace.leaf_scratch is not None else ""),
             "bound": "mfma",
             "achieved": round(leaf_tflops, 2),
             "peak": MFMA_16BIT_PEAK_TFLOPS,
