@@ -35,11 +35,15 @@
 //
 // When Kb % 128 == 0 a 16x16x32 variant of the fast kernel (below, with its
 // own notes) runs instead; the 32x32x16 kernel covers the other fast shapes.
+// On that path a last partial round of tiles can be split along K into
+// fp32 parts in caller-owned scratch and added by tail_reduce_kernel (the
+// split-K tail, see launch_mfma16).
 //
 // Generic kernel (any Kb, any alignment): 256 x 256 tile, BK = 64, register-
 // staged loads with zero fill, double-buffered LDS; used for small or ragged
 // shapes where the fast kernel's preconditions fail.
 #include <algorithm>
+#include <atomic>
 
 #include "abi_common.h"
 #include "fastmm_device.h"
@@ -788,15 +792,15 @@ __global__ __launch_bounds__(256) void tail_reduce_kernel(const float* __restric
 
 // Compute units of the current device (cached per device; 0 if unknown).
 int compute_units() {
-  static int cached[64] = {};
+  static std::atomic<int> cached[64];  // zero-initialized
   int device = 0;
   if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 0;
-  if (cached[device] == 0) {
-    int units = 0;
+  int units = cached[device].load(std::memory_order_relaxed);
+  if (units == 0) {
     if (hipDeviceGetAttribute(&units, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return 0;
-    cached[device] = units;
+    cached[device].store(units, std::memory_order_relaxed);
   }
-  return cached[device];
+  return units;
 }
 
 // One workgroup per CU: `total` tiles run in ceil(total / CUs) rounds, and a
@@ -826,17 +830,29 @@ int64_t tail_scratch_bytes(const TailSplit& plan) {
 
 // ---------------------------------------------------------------- launchers
 
+// hipFuncSetAttribute (the dynamic LDS reservation above 64 KB) once per
+// kernel and device; `devices` holds one bit per device already configured
+// (atomic: first calls may race from several host threads, and setting the
+// attribute twice is harmless).
+template <class Kernel>
+int reserve_lds(Kernel kernel, int lds_bytes, std::atomic<uint64_t>& devices) {
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return fail(FASTMM_ERROR_LAUNCH, "leaf products: no current device");
+  const uint64_t bit = device >= 0 && device < 64 ? uint64_t{1} << device : 0;
+  if (bit != 0 && (devices.load(std::memory_order_acquire) & bit) != 0) return FASTMM_OK;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          lds_bytes) != hipSuccess) {
+    return fail(FASTMM_ERROR_LAUNCH, "leaf products: cannot reserve %d bytes of LDS", lds_bytes);
+  }
+  devices.fetch_or(bit, std::memory_order_release);
+  return FASTMM_OK;
+}
+
 template <class Kernel>
 int launch_tiles(Kernel kernel, int lds_bytes, const void* a, const void* b, void* p,
                  int64_t rank, int64_t mb, int64_t kb, int64_t nb, hipStream_t stream) {
-  static bool configured = false;  // one per kernel instantiation
-  if (!configured) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes) != hipSuccess) {
-      return fail(FASTMM_ERROR_LAUNCH, "leaf products: cannot reserve %d bytes of LDS", lds_bytes);
-    }
-    configured = true;
-  }
+  static std::atomic<uint64_t> configured{0};  // one per kernel instantiation
+  if (int status = reserve_lds(kernel, lds_bytes, configured)) return status;
   const int64_t tiles_m = ceil_div(mb, kTile);
   const int64_t tiles_n = ceil_div(nb, kTile);
   const int64_t total = tiles_m * tiles_n * rank;
@@ -864,24 +880,12 @@ bool mfma16_leaf_gemm_applies(int64_t mb, int64_t kb, int64_t nb) {
          (nb + kTile) * kb * 2 <= INT32_MAX;
 }
 
-template <class Kernel>
-int reserve_lds(Kernel kernel, int lds_bytes, bool& configured) {
-  if (!configured) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            lds_bytes) != hipSuccess) {
-      return fail(FASTMM_ERROR_LAUNCH, "leaf products: cannot reserve %d bytes of LDS", lds_bytes);
-    }
-    configured = true;
-  }
-  return FASTMM_OK;
-}
-
 // The 16x16x32 kernel over all tiles, with the split-K tail when scratch
 // holds its partial sums (otherwise the tail runs as whole tiles).
 template <int kIn, int kOut>
 int launch_mfma16(const void* a, const void* b, void* p, int64_t rank, int64_t mb, int64_t kb, int64_t nb,
                   void* scratch, int64_t scratch_bytes, hipStream_t stream) {
-  static bool main_ready = false, partial_ready = false;
+  static std::atomic<uint64_t> main_ready{0}, partial_ready{0};
   auto* main_kernel = mfma16::leaf_gemm_kernel<kIn, kOut, false>;
   auto* partial_kernel = mfma16::leaf_gemm_kernel<kIn, kFP32, true>;
   if (int status = reserve_lds(main_kernel, mfma16::LDS_BYTES, main_ready)) return status;

@@ -192,3 +192,27 @@ def test_leaf_products_within_fp32_accumulation_bound(dims, operand_dtype, produ
         bound = bound + np.abs(exact.astype(np.float64)) * 2.0**-8 + 2.0**-126
     for got in runs:
         assert np.all(np.abs(got.float().cpu().numpy().astype(np.float64) - exact) <= bound)
+
+
+def test_leaf_scratch_sizes_follow_the_tail_plan() -> None:
+    """The split-K tail plan: with one 256x256 tile per CU per round, a last round of
+    `tail = tiles % CUs` tiles filling at most half the CUs is split along K into
+    min(4, CUs // tail, Kb // 128) parts, each a 256 KB fp32 tile of scratch."""
+    cus = torch.cuda.get_device_properties(DEVICE).multi_processor_count
+
+    def expected(rank, mb, kb, nb):
+        tiles = rank * -(-mb // 256) * -(-nb // 256)
+        tail = tiles % cus
+        if tail == 0:
+            return 0
+        split = min(4, cus // tail, kb // 128)
+        return tail * split * 256 * 256 * 4 if split >= 2 else 0
+
+    for dims in ((7, 4107, 6144, 2304), (7, 2048, 2048, 6144), (48, 2048, 2048, 2048), (1, 256, 1024, 256),
+                 (3, 2560, 256, 2560), (7, 4107, 128, 2304), (7, 4352, 6144, 2304)):
+        rank, mb, kb, nb = dims
+        got = _stages.leaf_scratch_bytes(rank, torch.float16, torch.float16, mb, kb, nb, DEVICE)
+        assert got == expected(rank, mb, kb, nb), dims
+    # shapes off the 16x16x32 path need none
+    assert _stages.leaf_scratch_bytes(7, torch.float16, torch.float16, 4107, 6150, 2304, DEVICE) == 0
+    assert _stages.leaf_scratch_bytes(7, torch.float16, torch.float16, 4107, 6144, 2300, DEVICE) == 0
