@@ -37,7 +37,7 @@
 // own notes) runs instead; the 32x32x16 kernel covers the other fast shapes.
 // On that path a last partial round of tiles can be split along K into
 // fp32 parts in caller-owned scratch and added by tail_reduce_kernel (the
-// split-K tail, see launch_mfma16).
+// split-K tail, see tail_split and launch_mfma16).
 //
 // Generic kernel (any Kb, any alignment): 256 x 256 tile, BK = 64, register-
 // staged loads with zero fill, double-buffered LDS; used for small or ragged
@@ -804,11 +804,14 @@ int compute_units() {
 }
 
 // One workgroup per CU: `total` tiles run in ceil(total / CUs) rounds, and a
-// last round of `tail` < CUs tiles leaves CUs idle for a whole tile time. When
-// the tail fills at most half the CUs, its tiles are split along K into
-// `split` = min(4, CUs / tail, groups of 4 slices) parts run side by side,
-// then added by tail_reduce_kernel: the last round takes ~1/split of a tile
-// time plus the reduction.
+// last round of `tail` < CUs tiles leaves CUs idle for a whole tile time. The
+// tail's tiles are split along K into `split` parts run side by side, then
+// added by tail_reduce_kernel: the last round takes ~1/split of a tile time
+// plus the reduction. split = min(8, groups of 4 slices, 3/4 CUs / tail), and
+// no split below 2. The 3/4 matters: a round that leaves CUs idle runs at a
+// higher clock (the chip is power-limited), so on MI355X a split filling every
+// CU lost ~5 % against whole tiles (tail of 128 tiles in 2 parts), while
+// splits over at most 3/4 of the CUs gained 2-25 %, most for small tails.
 struct TailSplit {
   int64_t main_tiles, tail, split;
 };
@@ -819,7 +822,7 @@ TailSplit tail_split(int64_t total, int64_t kb) {
   if (cus <= 0) return {total, 0, 1};
   const int64_t tail = total % cus;
   if (tail == 0) return {total, 0, 1};
-  const int64_t split = std::min<int64_t>({4, cus / tail, groups});
+  const int64_t split = std::min<int64_t>({8, groups, 3 * cus / (4 * tail)});
   if (split < 2) return {total, 0, 1};
   return {total - tail, tail, split};
 }

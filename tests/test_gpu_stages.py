@@ -196,8 +196,8 @@ def test_leaf_products_within_fp32_accumulation_bound(dims, operand_dtype, produ
 
 def test_leaf_scratch_sizes_follow_the_tail_plan() -> None:
     """The split-K tail plan: with one 256x256 tile per CU per round, a last round of
-    `tail = tiles % CUs` tiles filling at most half the CUs is split along K into
-    min(4, CUs // tail, Kb // 128) parts, each a 256 KB fp32 tile of scratch."""
+    `tail = tiles % CUs` tiles is split along K into min(8, Kb // 128, 3*CUs // (4*tail))
+    parts (none below 2), each a 256 KB fp32 tile of scratch."""
     cus = torch.cuda.get_device_properties(DEVICE).multi_processor_count
 
     def expected(rank, mb, kb, nb):
@@ -205,11 +205,14 @@ def test_leaf_scratch_sizes_follow_the_tail_plan() -> None:
         tail = tiles % cus
         if tail == 0:
             return 0
-        split = min(4, cus // tail, kb // 128)
+        split = min(8, kb // 128, 3 * cus // (4 * tail))
         return tail * split * 256 * 256 * 4 if split >= 2 else 0
 
+    # C3 (tail 47), C2 (64), whole rounds, one tile, K too short, split capped by
+    # Kb, a tail of 128 (no split), 24 (split 8), 16 (capped at 8)
     for dims in ((7, 4107, 6144, 2304), (7, 2048, 2048, 6144), (48, 2048, 2048, 2048), (1, 256, 1024, 256),
-                 (3, 2560, 256, 2560), (7, 4107, 128, 2304), (7, 4352, 6144, 2304)):
+                 (3, 2560, 256, 2560), (7, 4107, 128, 2304), (7, 4352, 6144, 2304), (48, 1100, 2048, 2048),
+                 (7, 1280, 14336, 2048), (48, 2816, 3072, 256)):
         rank, mb, kb, nb = dims
         got = _stages.leaf_scratch_bytes(rank, torch.float16, torch.float16, mb, kb, nb, DEVICE)
         assert got == expected(rank, mb, kb, nb), dims
