@@ -35,9 +35,11 @@
 //
 // When Kb % 128 == 0 a 16x16x32 variant of the fast kernel (below, with its
 // own notes) runs instead; the 32x32x16 kernel covers the other fast shapes.
-// On that path a last partial round of tiles can be split along K into
-// fp32 parts in caller-owned scratch and added by tail_reduce_kernel (the
-// split-K tail, see tail_split and launch_mfma16).
+// On that path, 16-bit products over more than one round of tiles run on its
+// persistent form (one workgroup per CU streaming slices across tile
+// boundaries, see persistent_kernel), and a last partial round of tiles can
+// be split along K into fp32 parts in caller-owned scratch and added by
+// tail_reduce_kernel (the split-K tail, see tail_split and launch_mfma16).
 //
 // Generic kernel (any Kb, any alignment): 256 x 256 tile, BK = 64, register-
 // staged loads with zero fill, double-buffered LDS; used for small or ragged
@@ -627,6 +629,328 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
   }
 }
 
+
+// Persistent variant for 16-bit products (Kb >= 256): gridDim.x workgroups
+// (a multiple of 8, one per CU) walk the tiles of their XCD's range (the same
+// range decode_tile gives), gridDim.x / 8 tiles apart. One continuous slice
+// stream: in a tile's last four slices the refills already fetch the next
+// tile's first four, so a tile starts without waiting for memory. The output
+// leaves through a 32 KB staging area after the 128 KB ring, in four chunks of
+// 64 rows (32 from each half of the tile, so every wave writes every chunk;
+// 16-byte chunks XOR-swizzled by row: conflict-free 8-byte writes), as full
+// 512-byte row segments. Every wave issues exactly 32 16-byte buffer
+// stores per tile (rows or columns past the leaf get an out-of-range offset
+// and write nothing), and the first two waits of the next tile let those
+// stores stay in flight (vmcnt 48 instead of 16): they drain under its MFMAs.
+// The prologue issues 32 stores that write nothing, so every tile starts with
+// the same count of operations in flight.
+constexpr int RING_BYTES = STAGES * STAGE_HALVES * 2;                      // 128 KB
+constexpr int STAGE_ROWS = 64;
+constexpr int PERSISTENT_LDS_BYTES = RING_BYTES + STAGE_ROWS * kTile * 2;  // 160 KB
+constexpr int kStoresPerTile = 32;  // per wave: 4 chunks x 8 passes
+
+__device__ __forceinline__ void persistent_tiles(int wg, int grid, int total, int& first, int& stride,
+                                                 int& count) {
+  constexpr int kXcds = 8;
+  const int q = total / kXcds, r = total - q * kXcds;
+  const int x = wg % kXcds, j = wg / kXcds;
+  const int start = x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q;
+  const int tiles = x < r ? q + 1 : q;
+  stride = grid / kXcds;
+  first = start + j;
+  count = j < tiles ? (tiles - j + stride - 1) / stride : 0;
+}
+
+typedef unsigned uint4v __attribute__((ext_vector_type(4)));
+typedef unsigned uint2v __attribute__((ext_vector_type(2)));
+
+// Two values rounded to the 16-bit product type, packed (first in the low
+// half). FP16 uses the packed conversion (round to nearest even, as the
+// scalar one); BF16 the shared rounding helper.
+template <int kOut>
+__device__ __forceinline__ unsigned pack2(float lo, float hi) {
+  if constexpr (kOut == kFP16) {
+    typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+    const half2v v = {static_cast<_Float16>(lo), static_cast<_Float16>(hi)};
+    return __builtin_bit_cast(unsigned, v);
+  } else {
+    return static_cast<unsigned>(from_f32<kOut>(lo)) | (static_cast<unsigned>(from_f32<kOut>(hi)) << 16);
+  }
+}
+
+template <int kIn, int kOut>
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void persistent_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B, uint16_t* __restrict__ P,
+                       int Mb, int Nb, int Kb, int tiles_m, int tiles_n, int total_tiles) {
+  extern __shared__ __attribute__((aligned(16))) half_t smem[];
+  int first, stride, count;
+  persistent_tiles(blockIdx.x, gridDim.x, total_tiles, first, stride, count);
+  if (count == 0) return;
+  const int nk = Kb / BK;  // a multiple of 4, at least 8 (checked by the launcher)
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // Load descriptor of the tile whose slices are being fetched (as in
+  // leaf_gemm_kernel; logical < 0: no tile, every lane out of range, so the
+  // loads read nothing and zero-fill their ring slots).
+  constexpr unsigned kOutOfRange = 0x80000000u;
+  constexpr unsigned kSegmentBytes = 64 * kSlab * 2;
+  const unsigned lane_base =
+      static_cast<unsigned>(((wave * 16 + (lane >> 2)) * kSlab + ((lane & 3) ^ ((lane >> 4) & 3)) * 8) * 2);
+  __amdgpu_buffer_rsrc_t a_rsrc, b_rsrc;
+  unsigned a_off[SEGMENTS], b_off[SEGMENTS];
+  auto set_loads = [&](int logical) __attribute__((always_inline)) {
+    const bool none = logical < 0;
+    int leaf, tm, tn;
+    tile_of(none ? 0 : logical, tiles_m, tiles_n, 8, leaf, tm, tn);
+    a_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(A + static_cast<int64_t>(leaf) * Mb * Kb), 0,
+                                               Mb * Kb * 2, 0x00020000);
+    b_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(B + static_cast<int64_t>(leaf) * Nb * Kb), 0,
+                                               Nb * Kb * 2, 0x00020000);
+    const unsigned a_limit = none ? 0u : static_cast<unsigned>(Mb * kSlab * 2);
+    const unsigned b_limit = none ? 0u : static_cast<unsigned>(Nb * kSlab * 2);
+    const unsigned a_first = lane_base + static_cast<unsigned>(tm * kTile * kSlab * 2);
+    const unsigned b_first = lane_base + static_cast<unsigned>(tn * kTile * kSlab * 2);
+#pragma unroll
+    for (int q = 0; q < SEGMENTS; ++q) {
+      const unsigned a = a_first + q * kSegmentBytes, b = b_first + q * kSegmentBytes;
+      a_off[q] = a < a_limit ? a : kOutOfRange;
+      b_off[q] = b < b_limit ? b : kOutOfRange;
+    }
+  };
+
+  const int fr = lane & 15, fc = lane >> 4;
+  const int rd = fr * BK + ((fc ^ ((fr >> 2) & 3)) << 3);
+  unsigned base_a[2], base_b[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    base_a[h] = (unsigned)(uintptr_t)(lds_ptr)(smem + h * 2 * STAGE_HALVES + wm * 128 * BK + rd);
+    base_b[h] = (unsigned)(uintptr_t)(lds_ptr)(smem + h * 2 * STAGE_HALVES + kTile * BK + wn * 128 * BK + rd);
+  }
+
+  half8 fa[2][FM], fb[2][FN];
+  float4v acc[FM][FN];  // never zeroed: a tile's first MFMAs take srcC = 0
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      fa[s][i] = half8{};
+      fb[s][i] = half8{};
+    }
+
+  // idx 0..3: A' segments, 4..7: B' segments of slice kt of the descriptor's tile
+  auto load_one = [&](int kt, int slot, int idx) __attribute__((always_inline)) {
+    const bool b_side = idx >= 4;
+    const int q = idx & 3;
+    half_t* dst = smem + slot * STAGE_HALVES + (b_side ? kTile * BK : 0) + (q * 4 + wave) * 16 * BK;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(b_side ? b_rsrc : a_rsrc, (lds_ptr)(dst), 16,
+                                             b_side ? b_off[q] : a_off[q], kt * (b_side ? Nb : Mb) * kSlab * 2,
+                                             0, 0);
+  };
+#define FASTMM_READ(kSlotSrc, kSet, r)                                                              \
+  do {                                                                                              \
+    if constexpr ((r) < 8)                                                                          \
+      asm volatile("ds_read_b128 %0, %1 offset:%2"                                                  \
+                   : "+v"(fa[kSet][(r)])                                                            \
+                   : "v"(base_a[(kSlotSrc) / 2]), "i"((((kSlotSrc) % 2) * STAGE_HALVES + (r) * 16 * BK) * 2)); \
+    else                                                                                            \
+      asm volatile("ds_read_b128 %0, %1 offset:%2"                                                  \
+                   : "+v"(fb[kSet][(r) - 8])                                                        \
+                   : "v"(base_b[(kSlotSrc) / 2]),                                                   \
+                     "i"((((kSlotSrc) % 2) * STAGE_HALVES + ((r) - 8) * 16 * BK) * 2));             \
+  } while (0)
+#define FASTMM_MFMA(kSet, q)                                                                        \
+  do {                                                                                              \
+    if constexpr (kFirst && kIn == kBF16)                                                           \
+      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0"                                         \
+                   : "=a"(acc[(q) / 8][(q) % 8])                                                    \
+                   : "v"(fb[kSet][(q) % 8]), "v"(fa[kSet][(q) / 8]));                               \
+    else if constexpr (kFirst)                                                                      \
+      asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, 0"                                          \
+                   : "=a"(acc[(q) / 8][(q) % 8])                                                    \
+                   : "v"(fb[kSet][(q) % 8]), "v"(fa[kSet][(q) / 8]));                               \
+    else if constexpr (kIn == kBF16)                                                                \
+      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"                                        \
+                   : "+a"(acc[(q) / 8][(q) % 8])                                                    \
+                   : "v"(fb[kSet][(q) % 8]), "v"(fa[kSet][(q) / 8]));                               \
+    else                                                                                            \
+      asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0"                                         \
+                   : "+a"(acc[(q) / 8][(q) % 8])                                                    \
+                   : "v"(fb[kSet][(q) % 8]), "v"(fa[kSet][(q) / 8]));                               \
+  } while (0)
+#define FASTMM_GROUP(g)                                                                             \
+  do {                                                                                              \
+    FASTMM_MFMA(kSet, 4 * (g));                                                                     \
+    FASTMM_MFMA(kSet, 4 * (g) + 1);                                                                 \
+    if constexpr (kNext) FASTMM_READ(kNextSlot, 1 - kSet, (g));                                     \
+    FASTMM_MFMA(kSet, 4 * (g) + 2);                                                                 \
+    FASTMM_MFMA(kSet, 4 * (g) + 3);                                                                 \
+    if constexpr (kLoad && (g) % 2 == 1) load_one(load_kt, kSlot, (g) / 2);                         \
+  } while (0)
+#define FASTMM_TIE(i)                                                                               \
+  asm volatile("" : "+a"(acc[i][0]), "+a"(acc[i][1]), "+a"(acc[i][2]), "+a"(acc[i][3]),             \
+                    "+a"(acc[i][4]), "+a"(acc[i][5]), "+a"(acc[i][6]), "+a"(acc[i][7]))
+  auto fence = [&]() __attribute__((always_inline)) {
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+    FASTMM_TIE(0); FASTMM_TIE(1); FASTMM_TIE(2); FASTMM_TIE(3);
+    FASTMM_TIE(4); FASTMM_TIE(5); FASTMM_TIE(6); FASTMM_TIE(7);
+  };
+
+  // One slice in ring slot kSlot (fragments in register set kSlot % 2): kLoad
+  // refills the slot with slice load_kt of the descriptor's tile; kNext reads
+  // the next slice's fragments; the wait leaves kWait operations in flight
+  // (16: the loads of the slices three and four ahead; 48: those and a tile's
+  // 32 stores) so that the slice two ahead is resident; kFirst starts the
+  // accumulators.
+  auto step = [&](int load_kt, auto slot_tag, auto load_tag, auto next_tag, auto wait_tag, auto first_tag)
+      __attribute__((always_inline)) {
+    constexpr int kSlot = decltype(slot_tag)::value;
+    constexpr bool kLoad = decltype(load_tag)::value;
+    constexpr bool kNext = decltype(next_tag)::value;
+    constexpr int kWait = decltype(wait_tag)::value;
+    constexpr bool kFirst = decltype(first_tag)::value;
+    constexpr int kSet = kSlot % 2, kNextSlot = (kSlot + 1) % STAGES;
+    FASTMM_GROUP(0); FASTMM_GROUP(1); FASTMM_GROUP(2); FASTMM_GROUP(3);
+    FASTMM_GROUP(4); FASTMM_GROUP(5); FASTMM_GROUP(6); FASTMM_GROUP(7);
+    FASTMM_GROUP(8); FASTMM_GROUP(9); FASTMM_GROUP(10); FASTMM_GROUP(11);
+    FASTMM_GROUP(12); FASTMM_GROUP(13); FASTMM_GROUP(14); FASTMM_GROUP(15);
+    if constexpr (kWait == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    else if constexpr (kWait == 48) asm volatile("s_waitcnt vmcnt(48)" ::: "memory");
+    else static_assert(kWait < 0, "unsupported vmcnt");
+    if constexpr (kNext) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    fast::barrier();
+  };
+  // A tile's first four slices (refilled with its slices 4..7; the first two
+  // waits allow the previous tile's stores in flight).
+  auto first_group = [&]() __attribute__((always_inline)) {
+    step(4, Int<0>{}, Bool<true>{}, Bool<true>{}, Int<48>{}, Bool<true>{});
+    step(5, Int<1>{}, Bool<true>{}, Bool<true>{}, Int<48>{}, Bool<false>{});
+    step(6, Int<2>{}, Bool<true>{}, Bool<true>{}, Int<16>{}, Bool<false>{});
+    step(7, Int<3>{}, Bool<true>{}, Bool<true>{}, Int<16>{}, Bool<false>{});
+    fence();
+  };
+  auto steady_group = [&](int load_kt) __attribute__((always_inline)) {
+    step(load_kt, Int<0>{}, Bool<true>{}, Bool<true>{}, Int<16>{}, Bool<false>{});
+    step(load_kt + 1, Int<1>{}, Bool<true>{}, Bool<true>{}, Int<16>{}, Bool<false>{});
+    step(load_kt + 2, Int<2>{}, Bool<true>{}, Bool<true>{}, Int<16>{}, Bool<false>{});
+    step(load_kt + 3, Int<3>{}, Bool<true>{}, Bool<true>{}, Int<16>{}, Bool<false>{});
+    fence();
+  };
+  // A tile's last four slices: the refills fetch slices 0..3 of the next tile
+  // (the descriptor was switched), and the last step reads no fragments, so
+  // both fragment sets are free in the epilogue.
+  auto boundary_group = [&]() __attribute__((always_inline)) {
+    step(0, Int<0>{}, Bool<true>{}, Bool<true>{}, Int<16>{}, Bool<false>{});
+    step(1, Int<1>{}, Bool<true>{}, Bool<true>{}, Int<16>{}, Bool<false>{});
+    step(2, Int<2>{}, Bool<true>{}, Bool<true>{}, Int<16>{}, Bool<false>{});
+    step(3, Int<3>{}, Bool<true>{}, Bool<false>{}, Int<16>{}, Bool<false>{});
+    fence();
+  };
+  // Slice-0 fragments (ring slot 0) into register set 0; every wave's reads
+  // done before slot 0 is refilled.
+  auto read_first_slice = [&]() __attribute__((always_inline)) {
+    constexpr int kSrc = 0, kDst = 0;
+    FASTMM_READ(kSrc, kDst, 0); FASTMM_READ(kSrc, kDst, 1); FASTMM_READ(kSrc, kDst, 2); FASTMM_READ(kSrc, kDst, 3);
+    FASTMM_READ(kSrc, kDst, 4); FASTMM_READ(kSrc, kDst, 5); FASTMM_READ(kSrc, kDst, 6); FASTMM_READ(kSrc, kDst, 7);
+    FASTMM_READ(kSrc, kDst, 8); FASTMM_READ(kSrc, kDst, 9); FASTMM_READ(kSrc, kDst, 10); FASTMM_READ(kSrc, kDst, 11);
+    FASTMM_READ(kSrc, kDst, 12); FASTMM_READ(kSrc, kDst, 13); FASTMM_READ(kSrc, kDst, 14); FASTMM_READ(kSrc, kDst, 15);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    fast::barrier();
+  };
+
+  const unsigned stage_base = (unsigned)(uintptr_t)(lds_ptr)(smem) + RING_BYTES;
+  set_loads(first);
+#pragma unroll
+  for (int s = 0; s < STAGES; ++s)
+#pragma unroll
+    for (int idx = 0; idx < 8; ++idx) load_one(s, s, idx);
+  {
+    // stores that write nothing (no records), in the place of a previous tile's
+    const __amdgpu_buffer_rsrc_t none = __builtin_amdgcn_make_buffer_rsrc(P, 0, 0, 0x00020000);
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int q = 0; q < kStoresPerTile; ++q)
+      __builtin_amdgcn_raw_buffer_store_b128(uint4v{0, 0, 0, 0}, none, kOutOfRange, 0, 0);
+    asm volatile("" ::: "memory");
+  }
+  asm volatile("s_waitcnt vmcnt(48)" ::: "memory");  // slices 0 and 1 resident
+  fast::barrier();
+  read_first_slice();
+
+  for (int t = 0; t < count; ++t) {
+    const int logical = first + t * stride;
+    first_group();
+    for (int kt = 4; kt < nk - 4; kt += 4) steady_group(kt + 4);
+    set_loads(t + 1 < count ? logical + stride : -1);
+    boundary_group();
+
+    // Epilogue: four chunks of 64 rows through the staging area.
+    int leaf, tm, tn;
+    tile_of(logical, tiles_m, tiles_n, 8, leaf, tm, tn);
+    const unsigned m0 = tm * kTile, n0 = tn * kTile;
+    const __amdgpu_buffer_rsrc_t p_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        P + static_cast<int64_t>(leaf) * Mb * Nb, 0, Mb * Nb * 2, 0x00020000);
+    // lane recomputed here (every lane is active), so no lane-derived value
+    // stays live across the K loop
+    int lane_now;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane_now));
+    const int er = lane_now & 15, eg = lane_now >> 4;
+    const int tid_now = wave * 64 + lane_now;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      // Chunk c: tile rows 32c .. 32c + 31 of each half (wm = 0, 1), that is
+      // accumulator rows i = 2c, 2c + 1 of every wave. Staging row
+      // wm*32 + ii*16 + er holds tile row wm*128 + (2c + ii)*16 + er; lane
+      // (er, eg) writes columns wn*128 + j*16 + 4*eg .. +3 (8 bytes).
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii) {
+        const int i = 2 * c + ii;
+        const unsigned row = wm * 32 + ii * 16 + er;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const unsigned chunk = wn * 16 + 2 * j + (eg >> 1);
+          const unsigned at = stage_base + row * (kTile * 2) + ((chunk ^ (row & 15)) << 4) + ((eg & 1) << 3);
+          const uint2v v = {pack2<kOut>(acc[i][j][0], acc[i][j][1]), pack2<kOut>(acc[i][j][2], acc[i][j][3])};
+          asm volatile("ds_write_b64 %0, %1" : : "v"(at), "v"(v) : "memory");
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      fast::barrier();
+      // two halves of four 16-byte reads, then their stores
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        uint4v staged[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const unsigned row = (half * 4 + h) * 8 + (tid_now >> 5), chunk = tid_now & 31;
+          const unsigned at = stage_base + row * (kTile * 2) + ((chunk ^ (row & 15)) << 4);
+          asm volatile("ds_read_b128 %0, %1" : "=v"(staged[h]) : "v"(at) : "memory");
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const unsigned sr = (half * 4 + h) * 8 + (tid_now >> 5);
+          const unsigned row = m0 + (sr >> 5) * 128 + 32 * c + (sr & 31);
+          const unsigned col = n0 + (tid_now & 31) * 8;
+          const bool inside = (row < static_cast<unsigned>(Mb)) & (col < static_cast<unsigned>(Nb));
+          const unsigned off = inside ? (row * static_cast<unsigned>(Nb) + col) * 2 : kOutOfRange;
+          __builtin_amdgcn_raw_buffer_store_b128(staged[h], p_rsrc, off, 0, 0);
+        }
+        asm volatile("" ::: "memory");
+      }
+      asm volatile("" ::: "memory");
+      if (c < 3) fast::barrier();  // every wave has read the chunk before the next is written
+    }
+    read_first_slice();
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last (empty) refills have landed in LDS
+#undef FASTMM_READ
+#undef FASTMM_MFMA
+#undef FASTMM_GROUP
+#undef FASTMM_TIE
+}
+
 }  // namespace mfma16
 
 // -------------------------------------------------------------- generic path
@@ -851,6 +1175,30 @@ int reserve_lds(Kernel kernel, int lds_bytes, std::atomic<uint64_t>& devices) {
   return FASTMM_OK;
 }
 
+// The same reservation for an optional kernel: false when the device refuses
+// it, leaving no error behind (the runtime's last error is cleared) and not
+// asking that device again.
+template <class Kernel>
+bool try_reserve_lds(Kernel kernel, int lds_bytes, std::atomic<uint64_t>& granted,
+                     std::atomic<uint64_t>& refused) {
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) {
+    (void)hipGetLastError();
+    return false;
+  }
+  const uint64_t bit = uint64_t{1} << device;
+  if ((granted.load(std::memory_order_acquire) & bit) != 0) return true;
+  if ((refused.load(std::memory_order_acquire) & bit) != 0) return false;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          lds_bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    refused.fetch_or(bit, std::memory_order_release);
+    return false;
+  }
+  granted.fetch_or(bit, std::memory_order_release);
+  return true;
+}
+
 template <class Kernel>
 int launch_tiles(Kernel kernel, int lds_bytes, const void* a, const void* b, void* p,
                  int64_t rank, int64_t mb, int64_t kb, int64_t nb, hipStream_t stream) {
@@ -905,7 +1253,24 @@ int launch_mfma16(const void* a, const void* b, void* p, int64_t rank, int64_t m
   const half_t* B = static_cast<const half_t*>(b);
   const int M = static_cast<int>(mb), N = static_cast<int>(nb), K = static_cast<int>(kb);
   const int TM = static_cast<int>(tiles_m), TN = static_cast<int>(tiles_n);
-  if (plan.main_tiles > 0) {
+  // More than one round of whole tiles: the persistent kernel (16-bit
+  // products, at least 8 slices, 32-bit store offsets, and the 160 KB LDS
+  // reservation granted; otherwise one workgroup per tile).
+  bool persistent = false;
+  if constexpr (kOut != kFP32) {
+    static std::atomic<uint64_t> persistent_granted{0}, persistent_refused{0};
+    const int64_t grid = compute_units() / 8 * 8;
+    persistent = grid >= 8 && plan.main_tiles > grid && kb >= 8 * mfma16::BK && mb * nb * 2 <= INT32_MAX &&
+                 try_reserve_lds(mfma16::persistent_kernel<kIn, kOut>, mfma16::PERSISTENT_LDS_BYTES,
+                                 persistent_granted, persistent_refused);
+    if (persistent) {
+      mfma16::persistent_kernel<kIn, kOut>
+          <<<dim3(static_cast<unsigned>(grid)), kGemmThreads, mfma16::PERSISTENT_LDS_BYTES, stream>>>(
+              A, B, static_cast<uint16_t*>(p), M, N, K, TM, TN, static_cast<int>(plan.main_tiles));
+      if (int status = check_launch("leaf products")) return status;
+    }
+  }
+  if (!persistent && plan.main_tiles > 0) {
     main_kernel<<<dim3(static_cast<unsigned>(plan.main_tiles)), kGemmThreads, mfma16::LDS_BYTES, stream>>>(
         A, B, p, M, N, K, TM, TN, static_cast<int>(plan.main_tiles), 0, 1, 1);
     if (int status = check_launch("leaf products")) return status;

@@ -147,8 +147,9 @@ def test_reconstruct_bit_exact(key, shape, product_dtype) -> None:
         # narrow columns, many leaves
         (7, 2048, 2304, 256), (2, 4107, 2304, 384), (48, 520, 512, 256), (17, 4000, 40, 256),
         (49, 1024, 1024, 512),
-        # split-K tail (with scratch): one tile in 4 K parts, ragged tiles, full rounds + a tail
-        (1, 256, 256, 1024), (2, 300, 520, 1024), (3, 2560, 2560, 256),
+        # split-K tail (with scratch): one tile in 8 K parts, ragged tiles, full rounds + a tail;
+        # two persistent rounds (16-bit products) + a tail in 6 parts
+        (1, 256, 256, 1024), (2, 300, 520, 1024), (3, 2560, 2560, 256), (3, 2300, 5120, 768),
     ),
 )
 @pytest.mark.parametrize(
@@ -219,3 +220,39 @@ def test_leaf_scratch_sizes_follow_the_tail_plan() -> None:
     # shapes off the 16x16x32 path need none
     assert _stages.leaf_scratch_bytes(7, torch.float16, torch.float16, 4107, 6150, 2304, DEVICE) == 0
     assert _stages.leaf_scratch_bytes(7, torch.float16, torch.float16, 4107, 6144, 2300, DEVICE) == 0
+
+
+@pytest.mark.parametrize(
+    ("rank", "mb", "kb", "nb", "scale", "dtype"),
+    (
+        (7, 1000, 384, 2776, 1.0, torch.float16),  # ragged rows and columns
+        (3, 2304, 1024, 4096, 30.0, torch.float16),  # fp16 overflow to infinity
+        (3, 2048, 256, 4096, 1e-3, torch.float16),  # fp16 subnormals; 8 slices, the minimum
+        (7, 1000, 384, 2776, 1.0, torch.bfloat16),
+    ),
+)
+def test_persistent_and_per_tile_kernels_agree_bitwise(rank, mb, kb, nb, scale, dtype) -> None:
+    """16-bit products over more tiles than compute units run on the persistent kernel;
+    the same leaves one at a time (fewer tiles than compute units) run one workgroup per
+    tile. Both compute each tile with the same MFMA sequence and the same rounding, so
+    the products agree bit for bit (no scratch: no split-K tail in either)."""
+    print(f"\n[case] persistent vs per-tile {(rank, mb, kb, nb)} {dtype} scale {scale}", flush=True)
+    cus = torch.cuda.get_device_properties(DEVICE).multi_processor_count
+    per_leaf = -(-mb // 256) * -(-nb // 256)
+    if not per_leaf <= cus < rank * per_leaf:
+        pytest.skip(f"{cus} compute units: the shape does not split into both paths")
+    g = torch.Generator().manual_seed(rank * mb + kb + nb)
+    a = (torch.randn((rank, mb, kb), generator=g) * scale).to(dtype).to(DEVICE)
+    b = (torch.randn((rank, nb, kb), generator=g) * scale).to(dtype).to(DEVICE)
+    together = torch.full((rank, mb, nb), float("nan"), device=DEVICE, dtype=dtype)
+    apart = torch.full((rank, mb, nb), float("nan"), device=DEVICE, dtype=dtype)
+    _stages.leaf_products(rank, a, b, together, mb, kb, nb)
+    for r in range(rank):
+        _stages.leaf_products(1, a[r : r + 1], b[r : r + 1], apart[r : r + 1], mb, kb, nb)
+    torch.cuda.synchronize()
+    assert not torch.isnan(together).any()
+    assert torch.equal(together.view(torch.int16), apart.view(torch.int16))
+    if scale > 1:
+        assert torch.isinf(together).any()
+    if scale < 1:
+        assert ((together != 0) & (together.abs() < 2.0**-14)).any()

@@ -83,7 +83,8 @@ def test_checker_on_accumulator_input_written_just_before() -> None:
 
 def test_main_loop_shape(assembly) -> None:
     for name, body in _kernels(assembly).items():
-        loop = re.search(r"; =>This Inner Loop Header.*?s_cbranch_scc1", body, re.DOTALL)
+        # the K loop: the whole-tile kernels' only loop, the persistent kernels' inner one
+        loop = re.search(r"; =>\s*This Inner Loop Header.*?s_cbranch_scc[01]", body, re.DOTALL)
         assert loop, name
         opcodes = [
             line.split(";", 1)[0].split()[0]
@@ -92,7 +93,8 @@ def test_main_loop_shape(assembly) -> None:
         ]
         count = lambda prefix: sum(op.startswith(prefix) for op in opcodes)  # noqa: E731
         # four slices per iteration: 64 MFMAs, 16 fragment reads, 8 refills each
-        mfma = "v_mfma_f32_16x16x32_bf16" if "ILi0E" in name.split("leaf_gemm_kernel", 1)[1][:6] else "v_mfma_f32_16x16x32_f16"
+        operand = re.search(r"kernelILi(\d)E", name).group(1)  # first template argument
+        mfma = "v_mfma_f32_16x16x32_bf16" if operand == "0" else "v_mfma_f32_16x16x32_f16"
         assert count(mfma) == 256, name
         assert count("ds_read_b128") == 64, name
         assert count("buffer_load_dwordx4") == 32, name
