@@ -96,12 +96,21 @@ def _median(values: list[float]) -> float:
     return ordered[len(ordered) // 2]
 
 
-def leaf_kernel_name(block_inner: int, compute: str) -> str:
-    """The leaf-GEMM kernel fastmm_leaf_products runs for the bench shapes (aligned
-    16-bit products): the 16x16x32 kernel when Kb % 128 == 0, else the 32x32x16 one."""
-    if block_inner % 128 == 0:
-        return f"fastmm::mfma16::leaf_gemm_kernel<{compute}, {compute}> (fastmm_leaf_products)"
-    return f"fastmm::fast::leaf_gemm_kernel<{compute}, {compute}> (fastmm_leaf_products)"
+def leaf_kernel_name(rank: int, mb: int, kb: int, nb: int, compute: str, cus: int, split_tail: bool) -> str:
+    """The main leaf-GEMM kernel fastmm_leaf_products runs for the bench shapes (aligned
+    16-bit products), by the library's launch rule: on the 16x16x32 path (Kb % 128 == 0)
+    the persistent kernel when the tiles left after the split-K tail exceed one round
+    (CUs rounded down to a multiple of 8), Kb >= 256 and a leaf's products fit 32-bit
+    offsets; else one workgroup per tile; the 32x32x16 kernel for other Kb."""
+    if kb % 128:
+        return f"fastmm::fast::leaf_gemm_kernel<{compute}, {compute}> (fastmm_leaf_products)"
+    tiles = rank * -(-mb // 256) * -(-nb // 256)
+    tail = tiles % cus
+    split = min(8, kb // 128, 3 * cus // (4 * tail)) if tail else 0
+    main = tiles - tail if split_tail and split >= 2 else tiles
+    if main > cus // 8 * 8 and kb >= 256 and mb * nb * 2 <= 2**31 - 1:
+        return f"fastmm::mfma16::persistent_kernel<{compute}, {compute}> (fastmm_leaf_products)"
+    return f"fastmm::mfma16::leaf_gemm_kernel<{compute}, {compute}> (fastmm_leaf_products)"
 
 
 def measured_traffic(config: str) -> float | None:
@@ -336,7 +345,11 @@ def main() -> int:
         "stages_ms": {name: round(v, 4) for name, v in stage_ms.items()},
         "packing_ms": round(pack_ms, 4),
         "roofline": {
-            "kernel": leaf_kernel_name(shape.block_inner, "bf16" if compute == torch.bfloat16 else "fp16")
+            "kernel": leaf_kernel_name(
+                plan.rank, shape.block_rows, shape.block_inner, shape.block_columns,
+                "bf16" if compute == torch.bfloat16 else "fp16",
+                torch.cuda.get_device_properties(device).multi_processor_count, workspace.leaf_scratch is not None,
+            )
             + (" + split-K tail (kPartial parts + tail_reduce_kernel); timed as the whole stage"
                if workspace.leaf_scratch is not None else ""),
             "bound": "mfma",
