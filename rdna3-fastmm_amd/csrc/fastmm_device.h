@@ -40,12 +40,14 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t bits) {
   return __uint_as_float(static_cast<uint32_t>(bits) << 16);
 }
 
-// fp32 -> bf16, round to nearest even; NaN stays a quiet NaN.
+// fp32 -> bf16, round to nearest even; NaN stays a quiet NaN. Both results
+// are computed and one selected (no branch: vectorized callers keep every
+// lane on one path).
 __device__ __forceinline__ uint16_t f32_to_bf16(float value) {
-  uint32_t bits = __float_as_uint(value);
-  if ((bits & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((bits >> 16) | 0x40u);
-  bits += 0x7fffu + ((bits >> 16) & 1u);
-  return static_cast<uint16_t>(bits >> 16);
+  const uint32_t bits = __float_as_uint(value);
+  const uint32_t quiet = (bits >> 16) | 0x40u;
+  const uint32_t rounded = (bits + 0x7fffu + ((bits >> 16) & 1u)) >> 16;
+  return static_cast<uint16_t>((bits & 0x7fffffffu) > 0x7f800000u ? quiet : rounded);
 }
 
 __device__ __forceinline__ float fp16_to_f32(uint16_t bits) {

@@ -71,16 +71,24 @@ __device__ __forceinline__ void tile_of(int logical, int tiles_m, int tiles_n, i
 }
 
 // Workgroups are dispatched round-robin over the 8 XCDs (workgroup w runs on
-// XCD w % 8); renumber so that each XCD works on a contiguous range of tiles
+// XCD w % 8); each XCD works on a contiguous range of the logical tiles
 // (tiles of one leaf share A'/B' rows in that XCD's L2): with q = total / 8
-// and r = total % 8, XCD x receives q + 1 workgroups if x < r, else q, and
-// takes the logical tiles starting at x*(q+1) (x < r) or r*(q+1) + (x-r)*q.
+// and r = total % 8, XCD x takes q + 1 tiles if x < r, else q, starting at
+// x*(q+1) (x < r) or r*(q+1) + (x-r)*q.
+constexpr int kXcds = 8;
+
+__device__ __forceinline__ void xcd_range(int total, int x, int& start, int& count) {
+  const int q = total / kXcds, r = total - q * kXcds;
+  start = x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q;
+  count = x < r ? q + 1 : q;
+}
+
+// One workgroup per tile: workgroup w takes tile w / 8 of its XCD's range.
 __device__ __forceinline__ void decode_tile(int wg, int total, int tiles_m, int tiles_n,
                                             int group, int& leaf, int& tm, int& tn) {
-  constexpr int kXcds = 8;
-  const int q = total / kXcds, r = total - q * kXcds;
-  const int x = wg % kXcds, i = wg / kXcds;
-  tile_of(x < r ? x * (q + 1) + i : r * (q + 1) + (x - r) * q + i, tiles_m, tiles_n, group, leaf, tm, tn);
+  int start, count;
+  xcd_range(total, wg % kXcds, start, count);
+  tile_of(start + wg / kXcds, tiles_m, tiles_n, group, leaf, tm, tn);
 }
 
 // 32x32x16 MFMA on 8 operand elements per lane, fp16 or bf16 (same register
@@ -649,13 +657,13 @@ constexpr int STAGE_ROWS = 64;
 constexpr int PERSISTENT_LDS_BYTES = RING_BYTES + STAGE_ROWS * kTile * 2;  // 160 KB
 constexpr int kStoresPerTile = 32;  // per wave: 4 chunks x 8 passes
 
+// Persistent workgroup wg of `grid` (a multiple of 8): tiles first,
+// first + stride, ... (count of them) of its XCD's range, stride = grid / 8.
 __device__ __forceinline__ void persistent_tiles(int wg, int grid, int total, int& first, int& stride,
                                                  int& count) {
-  constexpr int kXcds = 8;
-  const int q = total / kXcds, r = total - q * kXcds;
-  const int x = wg % kXcds, j = wg / kXcds;
-  const int start = x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q;
-  const int tiles = x < r ? q + 1 : q;
+  int start, tiles;
+  xcd_range(total, wg % kXcds, start, tiles);
+  const int j = wg / kXcds;
   stride = grid / kXcds;
   first = start + j;
   count = j < tiles ? (tiles - j + stride - 1) / stride : 0;
