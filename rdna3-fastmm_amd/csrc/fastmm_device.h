@@ -135,6 +135,17 @@ __device__ __forceinline__ void store16(uint16_t* p, const uint16_t (&in)[N]) {
   *reinterpret_cast<R*>(p) = raw;
 }
 
+// N 16-bit elements held as raw bits -> fp32.
+template <int kDType, int N>
+__device__ __forceinline__ Vec<N> raw_to_vec(const typename Raw16<N>::type& bits) {
+  uint16_t raw[N];
+  __builtin_memcpy(raw, &bits, sizeof(bits));
+  Vec<N> r;
+#pragma unroll
+  for (int i = 0; i < N; ++i) r.v[i] = to_f32<kDType>(raw[i]);
+  return r;
+}
+
 template <int kDType, int N>
 __device__ __forceinline__ Vec<N> load_vec(const uint16_t* p) {
   uint16_t raw[N];

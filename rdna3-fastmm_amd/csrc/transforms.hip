@@ -219,6 +219,35 @@ __global__ __launch_bounds__(block_threads<S>()) void reconstruct_kernel(
   const int64_t row = first / cols_b;
   const int64_t col = first - row * cols_b;
 
+  // Vector path with 16-bit products and R <= 64: every product (and bias)
+  // load is issued before the program runs and kept as raw bits (two
+  // registers per product at EPT = 4). Evaluated lazily, the late loads each
+  // come right before their first use, so every one waits a full memory round
+  // trip. Same arithmetic either way.
+  if constexpr (kVector && kProd != kFP32 && S::kRank <= 64) {
+    typedef typename Raw16<EPT>::type Raw;
+    const uint16_t* base = static_cast<const uint16_t*>(products) + first;
+    Raw raw[S::kRank];
+#pragma unroll
+    for (int r = 0; r < S::kRank; ++r) raw[r] = *reinterpret_cast<const Raw*>(base + static_cast<int64_t>(r) * plane);
+    Raw bias_raw[kBias ? s : 1];
+    if constexpr (kBias) {
+#pragma unroll
+      for (int j = 0; j < s; ++j) bias_raw[j] = *reinterpret_cast<const Raw*>(bias + j * cols_b + col);
+    }
+    asm volatile("" ::: "memory");  // no load moves below this point
+    auto load = [&](int r) -> Vec<EPT> { return raw_to_vec<kProd, EPT>(raw[r]); };
+    auto store = [&](int c, Vec<EPT> v) {
+      const int64_t out_row = (c / s) * rows_b + row;
+      if (out_row >= rows) return;
+      const int64_t out_col = (c % s) * cols_b + col;
+      if constexpr (kBias) v = v + raw_to_vec<kOut, EPT>(bias_raw[c % s]);
+      store_vec<kOut, EPT>(out + out_row * cols + out_col, v);
+    };
+    S::template output<Vec<EPT>>(load, store);
+    return;
+  }
+
   auto load = [&](int r) -> Vec<EPT> {
     return load_product<kProd, EPT>(products, static_cast<int64_t>(r) * plane + first);
   };
