@@ -101,16 +101,23 @@ def leaf_kernel_name(rank: int, mb: int, kb: int, nb: int, compute: str, cus: in
     16-bit products), by the library's launch rule: on the 16x16x32 path (Kb % 128 == 0)
     the persistent kernel when the tiles left after the split-K tail exceed one round
     (CUs rounded down to a multiple of 8), Kb >= 256 and a leaf's products fit 32-bit
-    offsets; else one workgroup per tile; the 32x32x16 kernel for other Kb."""
+    offsets; else one workgroup per tile; the 32x32x16 kernel for other Kb. A last tile
+    row of at most 16 rows goes to fastmm::thin::thin_rows_kernel when that takes the
+    256x256 tiles down a round and R * Nb <= 32768."""
     if kb % 128:
         return f"fastmm::fast::leaf_gemm_kernel<{compute}, {compute}> (fastmm_leaf_products)"
-    tiles = rank * -(-mb // 256) * -(-nb // 256)
+    tiles_n = -(-nb // 256)
+    with_row = rank * -(-mb // 256) * tiles_n
+    thin = (mb > 256 and 0 < mb % 256 <= 16 and rank * nb <= 32768
+            and -(-(with_row - rank * tiles_n) // cus) < -(-with_row // cus))
+    tiles = with_row - rank * tiles_n if thin else with_row
     tail = tiles % cus
     split = min(8, kb // 128, 3 * cus // (4 * tail)) if tail else 0
     main = tiles - tail if split_tail and split >= 2 else tiles
+    extra = " + thin_rows_kernel for the last tile row" if thin else ""
     if main > cus // 8 * 8 and kb >= 256 and mb * nb * 2 <= 2**31 - 1:
-        return f"fastmm::mfma16::persistent_kernel<{compute}, {compute}> (fastmm_leaf_products)"
-    return f"fastmm::mfma16::leaf_gemm_kernel<{compute}, {compute}> (fastmm_leaf_products)"
+        return f"fastmm::mfma16::persistent_kernel<{compute}, {compute}> (fastmm_leaf_products){extra}"
+    return f"fastmm::mfma16::leaf_gemm_kernel<{compute}, {compute}> (fastmm_leaf_products){extra}"
 
 
 def measured_traffic(config: str) -> float | None:
@@ -350,8 +357,8 @@ def main() -> int:
                 "bf16" if compute == torch.bfloat16 else "fp16",
                 torch.cuda.get_device_properties(device).multi_processor_count, workspace.leaf_scratch is not None,
             )
-            + (" + split-K tail (kPartial parts + tail_reduce_kernel); timed as the whole stage"
-               if workspace.leaf_scratch is not None else ""),
+            + (" + split-K tail (kPartial parts + tail_reduce_kernel) where the plan splits;"
+               " timed as the whole stage" if workspace.leaf_scratch is not None else ""),
             "bound": "mfma",
             "achieved": round(leaf_tflops, 2),
             "peak": MFMA_16BIT_PEAK_TFLOPS,

@@ -961,6 +961,94 @@ void persistent_kernel(const half_t* __restrict__ A, const half_t* __restrict__ 
 
 }  // namespace mfma16
 
+// ------------------------------------------------------- thin last tile row
+
+// When a leaf's last row of 256x256 tiles holds at most 16 rows (Mb % 256 in
+// 1..16, e.g. Mb = 4107), those tiles would run a whole tile's MFMAs for a few
+// rows and, in count, push the tiles past a round boundary (at Mb = 4107:
+// 1071 tiles, 47 past four rounds). They run here instead, as one 16-row
+// block: tiles of 64 columns (grid: column tiles x leaves), each wave 16
+// columns, operands straight from the K-slab planes into registers (16-byte
+// loads, four slices in flight). The strip reads all of B' once, so it pays
+// off only for a few rows and a small B' (leaf_plan decides). Each product is the same v_mfma_f32_16x16x32
+// sequence over the same 32-wide K slices, in the same operand order, as in
+// the 256 x 256 kernels, so the products are bit-identical.
+namespace thin {
+
+constexpr int kRows = 16, kCols = 64;
+using mfma16::uint4v;
+
+template <int kIn>
+__device__ __forceinline__ float4v mfma_16x16x32(uint4v a, uint4v b, float4v c) {
+  if constexpr (kIn == kBF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                    0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0,
+                                                   0, 0);
+  }
+}
+
+template <int kIn, int kOut>
+__global__ __launch_bounds__(kGemmThreads) void thin_rows_kernel(const half_t* __restrict__ A,
+                                                                 const half_t* __restrict__ B, void* __restrict__ P,
+                                                                 int Mb, int Nb, int Kb, int m0) {
+  const int leaf = blockIdx.y;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int fr = lane & 15, fk = lane >> 4;  // fragment row, 8-wide K chunk
+  // Fragment addresses in slab 0 of the leaf's planes. Rows or columns past
+  // the leaf read a clamped valid element: their products only reach output
+  // rows or columns that are not stored (row m of P needs only row m of A',
+  // column n only row n of B').
+  const half_t* a_base =
+      A + static_cast<int64_t>(leaf) * Mb * Kb + min(m0 + fr, Mb - 1) * kSlab + fk * 8;
+  const int col = blockIdx.x * kCols + wave * 16 + fr;
+  const half_t* b_base = B + static_cast<int64_t>(leaf) * Nb * Kb + min(col, Nb - 1) * kSlab + fk * 8;
+  // kDepth slices of fragments in flight, a ring of registers (nk is a
+  // multiple of 4 on this path; refills past the last slice re-read it). The
+  // loads are asm with explicit waits: compiler-placed waits at the loop head
+  // would drain the whole ring every iteration.
+  constexpr int kDepth = 4;
+  const int nk = Kb / kSlab;
+  uint4v bf[kDepth], af[kDepth];
+#pragma unroll
+  for (int d = 0; d < kDepth; ++d) bf[d] = af[d] = uint4v{0, 0, 0, 0};
+  auto fetch = [&](int slot, int kt) __attribute__((always_inline)) {
+    kt = kt < nk ? kt : nk - 1;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "+v"(bf[slot]) : "v"(b_base + static_cast<int64_t>(kt) * Nb * kSlab));
+    asm volatile("global_load_dwordx4 %0, %1, off" : "+v"(af[slot]) : "v"(a_base + static_cast<int64_t>(kt) * Mb * kSlab));
+  };
+#pragma unroll
+  for (int d = 0; d < kDepth; ++d) fetch(d, d);
+  float4v acc = {};
+  for (int kt = 0; kt < nk; kt += kDepth) {
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) {
+      // slot d landed, the other three slots' six loads may be in flight; the
+      // slot's registers are tied so the MFMA cannot move above the wait
+      static_assert(kDepth == 4, "vmcnt below is (kDepth - 1) * 2");
+      asm volatile("s_waitcnt vmcnt(6)" : "+v"(bf[d]), "+v"(af[d]) : : "memory");
+      acc = mfma_16x16x32<kIn>(bf[d], af[d], acc);  // operands (B', A'): lane l holds row l%16
+      fetch(d, kt + d + kDepth);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // element e of lane l: row m0 + l%16, column (16-column block) + 4*(l/16) + e
+  const int row = m0 + fr, out_col = blockIdx.x * kCols + wave * 16 + 4 * fk;
+  if (row >= Mb || out_col >= Nb) return;
+  const int64_t at = static_cast<int64_t>(leaf) * Mb * Nb + static_cast<int64_t>(row) * Nb + out_col;
+  if constexpr (kOut == kFP32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(P) + at) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  } else {
+    uint16_t h[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) h[e] = from_f32<kOut>(acc[e]);
+    store16<4>(static_cast<uint16_t*>(P) + at, h);
+  }
+}
+
+}  // namespace thin
+
 // -------------------------------------------------------------- generic path
 
 namespace generic {
@@ -1163,6 +1251,31 @@ int64_t tail_scratch_bytes(const TailSplit& plan) {
   return plan.tail * plan.split * kTile * kTile * static_cast<int64_t>(sizeof(float));
 }
 
+// The 16x16x32 path's launch plan: the split-K tail is planned on the
+// 256 x 256 tiles, and a last tile row of at most 16 rows (below a full one)
+// goes to thin_rows_kernel when that takes the tiles down a round and the
+// strip is cheap. The strip re-reads all of B' (R * Nb * Kb * 2 bytes), which
+// costs about R * Nb / 64K tile rounds at any Kb: on MI355X it saved 4 % of
+// the leaf stage at R * Nb = 16128 (rank 7, 8214 x 12288 x 4608) and lost
+// 1.4 % at 55296 (rank 48, same shape).
+constexpr int64_t kThinMaxRankColumns = 32768;
+
+struct LeafPlan {
+  int64_t tiles_m, tiles_n;  // 256 x 256 tiles (the thin row excluded)
+  bool thin;
+  TailSplit split;
+};
+
+LeafPlan leaf_plan(int64_t rank, int64_t mb, int64_t kb, int64_t nb) {
+  const int64_t rem = mb % kTile, tiles_n = ceil_div(nb, kTile);
+  const int64_t with_row = ceil_div(mb, kTile) * tiles_n * rank, without_row = with_row - tiles_n * rank;
+  const int64_t cus = compute_units();
+  const bool thin = mb > kTile && rem > 0 && rem <= thin::kRows && rank * nb <= kThinMaxRankColumns && cus > 0 &&
+                    ceil_div(without_row, cus) < ceil_div(with_row, cus);
+  const int64_t tiles_m = ceil_div(mb, kTile) - (thin ? 1 : 0);
+  return {tiles_m, tiles_n, thin, tail_split(rank * tiles_m * tiles_n, kb)};
+}
+
 // ---------------------------------------------------------------- launchers
 
 // hipFuncSetAttribute (the dynamic LDS reservation above 64 KB) once per
@@ -1249,10 +1362,13 @@ int launch_mfma16(const void* a, const void* b, void* p, int64_t rank, int64_t m
   auto* partial_kernel = mfma16::leaf_gemm_kernel<kIn, kFP32, true>;
   if (int status = reserve_lds(main_kernel, mfma16::LDS_BYTES, main_ready)) return status;
   if (int status = reserve_lds(partial_kernel, mfma16::LDS_BYTES, partial_ready)) return status;
-  const int64_t tiles_m = ceil_div(mb, kTile), tiles_n = ceil_div(nb, kTile);
+  if (ceil_div(mb, kTile) * ceil_div(nb, kTile) * rank > INT32_MAX / 4) {
+    return fail(FASTMM_ERROR_UNSUPPORTED, "leaf products: too many tiles");
+  }
+  const LeafPlan layout = leaf_plan(rank, mb, kb, nb);
+  const int64_t tiles_m = layout.tiles_m, tiles_n = layout.tiles_n;
   const int64_t total = tiles_m * tiles_n * rank;
-  if (total > INT32_MAX / 4) return fail(FASTMM_ERROR_UNSUPPORTED, "leaf products: too many tiles");
-  TailSplit plan = tail_split(total, kb);
+  TailSplit plan = layout.split;
   if (plan.tail > 0 && (scratch == nullptr || scratch_bytes < tail_scratch_bytes(plan) ||
                         !aligned_to(scratch, 16))) {
     plan = {total, 0, 1};
@@ -1283,15 +1399,23 @@ int launch_mfma16(const void* a, const void* b, void* p, int64_t rank, int64_t m
         A, B, p, M, N, K, TM, TN, static_cast<int>(plan.main_tiles), 0, 1, 1);
     if (int status = check_launch("leaf products")) return status;
   }
-  if (plan.tail == 0) return FASTMM_OK;
-  const int tail = static_cast<int>(plan.tail), split = static_cast<int>(plan.split);
-  const int base = static_cast<int>(plan.main_tiles);
-  partial_kernel<<<dim3(static_cast<unsigned>(tail * split)), kGemmThreads, mfma16::LDS_BYTES, stream>>>(
-      A, B, scratch, M, N, K, TM, TN, 0, base, tail, split);
-  if (int status = check_launch("leaf products (split-K tail)")) return status;
-  tail_reduce_kernel<kOut><<<dim3(kTile * kTile / 4 / 256, static_cast<unsigned>(tail)), 256, 0, stream>>>(
-      static_cast<const float*>(scratch), p, M, N, TM, TN, base, split);
-  return check_launch("leaf products (tail reduction)");
+  if (plan.tail > 0) {
+    const int tail = static_cast<int>(plan.tail), split = static_cast<int>(plan.split);
+    const int base = static_cast<int>(plan.main_tiles);
+    partial_kernel<<<dim3(static_cast<unsigned>(tail * split)), kGemmThreads, mfma16::LDS_BYTES, stream>>>(
+        A, B, scratch, M, N, K, TM, TN, 0, base, tail, split);
+    if (int status = check_launch("leaf products (split-K tail)")) return status;
+    tail_reduce_kernel<kOut><<<dim3(kTile * kTile / 4 / 256, static_cast<unsigned>(tail)), 256, 0, stream>>>(
+        static_cast<const float*>(scratch), p, M, N, TM, TN, base, split);
+    if (int status = check_launch("leaf products (tail reduction)")) return status;
+  }
+  if (layout.thin) {
+    thin::thin_rows_kernel<kIn, kOut>
+        <<<dim3(static_cast<unsigned>(ceil_div(nb, thin::kCols)), static_cast<unsigned>(rank)), kGemmThreads, 0,
+           stream>>>(A, B, p, M, N, K, static_cast<int>(tiles_m * kTile));
+    if (int status = check_launch("leaf products (thin tile row)")) return status;
+  }
+  return FASTMM_OK;
 }
 
 }  // namespace fastmm
@@ -1391,7 +1515,6 @@ extern "C" int fastmm_leaf_scratch_bytes(int rank, int operand_dtype, int produc
       !mfma16_leaf_gemm_applies(block_rows, block_inner, block_columns)) {
     return FASTMM_OK;
   }
-  const int64_t total = ceil_div(block_rows, kTile) * ceil_div(block_columns, kTile) * rank;
-  *bytes = tail_scratch_bytes(tail_split(total, block_inner));
+  *bytes = tail_scratch_bytes(leaf_plan(rank, block_rows, block_inner, block_columns).split);
   return FASTMM_OK;
 }

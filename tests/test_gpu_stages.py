@@ -198,11 +198,18 @@ def test_leaf_products_within_fp32_accumulation_bound(dims, operand_dtype, produ
 def test_leaf_scratch_sizes_follow_the_tail_plan() -> None:
     """The split-K tail plan: with one 256x256 tile per CU per round, a last round of
     `tail = tiles % CUs` tiles is split along K into min(8, Kb // 128, 3*CUs // (4*tail))
-    parts (none below 2), each a 256 KB fp32 tile of scratch."""
+    parts (none below 2), each a 256 KB fp32 tile of scratch. A last tile row that runs
+    in the thin-row kernel is not counted."""
     cus = torch.cuda.get_device_properties(DEVICE).multi_processor_count
 
     def expected(rank, mb, kb, nb):
-        tiles = rank * -(-mb // 256) * -(-nb // 256)
+        # a last tile row of at most 16 rows (below a full one) runs in its own kernel
+        # when that takes the tiles down a round and rank * Nb <= 32768
+        tiles_n = -(-nb // 256)
+        tiles = rank * -(-mb // 256) * tiles_n
+        if (mb > 256 and 0 < mb % 256 <= 16 and rank * nb <= 32768
+                and -(-(tiles - rank * tiles_n) // cus) < -(-tiles // cus)):
+            tiles -= rank * tiles_n
         tail = tiles % cus
         if tail == 0:
             return 0
@@ -213,7 +220,8 @@ def test_leaf_scratch_sizes_follow_the_tail_plan() -> None:
     # Kb, a tail of 128 (no split), 24 (split 8), 16 (capped at 8)
     for dims in ((7, 4107, 6144, 2304), (7, 2048, 2048, 6144), (48, 2048, 2048, 2048), (1, 256, 1024, 256),
                  (3, 2560, 256, 2560), (7, 4107, 128, 2304), (7, 4352, 6144, 2304), (48, 1100, 2048, 2048),
-                 (7, 1280, 14336, 2048), (48, 2816, 3072, 256)):
+                 (7, 1280, 14336, 2048), (48, 2816, 3072, 256), (7, 4112, 6144, 2304), (7, 4113, 6144, 2304),
+                 (48, 2054, 3072, 1152), (2, 2305, 256, 3328)):
         rank, mb, kb, nb = dims
         got = _stages.leaf_scratch_bytes(rank, torch.float16, torch.float16, mb, kb, nb, DEVICE)
         assert got == expected(rank, mb, kb, nb), dims
@@ -256,3 +264,43 @@ def test_persistent_and_per_tile_kernels_agree_bitwise(rank, mb, kb, nb, scale, 
         assert torch.isinf(together).any()
     if scale < 1:
         assert ((together != 0) & (together.abs() < 2.0**-14)).any()
+
+
+@pytest.mark.parametrize(
+    ("rank", "mb", "kb", "nb", "dtype", "product_dtype"),
+    (
+        (7, 4107, 1024, 2304, torch.float16, torch.float16),  # C3's 11-row edge
+        (2, 2320, 256, 3320, torch.float16, torch.float16),  # 16 rows, ragged columns, 8 slices
+        (2, 2320, 512, 3328, torch.bfloat16, torch.bfloat16),
+        (2, 2305, 384, 3328, torch.float16, torch.float32),  # one row, fp32 products
+    ),
+)
+def test_thin_tile_row_matches_full_tiles_bitwise(rank, mb, kb, nb, dtype, product_dtype) -> None:
+    """A last tile row of at most 16 rows runs in the thin-row kernel (when that takes the
+    tiles down a round). Padding the leaves with zero rows until that row holds more than
+    16 rows sends it through the 256x256 kernels instead; zero rows change no other row, and both kernels issue the
+    same MFMA sequence per product, so the real rows agree bit for bit."""
+    print(f"\n[case] thin tile row {(rank, mb, kb, nb)} {dtype} -> {product_dtype}", flush=True)
+    cus = torch.cuda.get_device_properties(DEVICE).multi_processor_count
+    tiles_n = -(-nb // 256)
+    tiles = rank * -(-mb // 256) * tiles_n
+    if not -(-(tiles - rank * tiles_n) // cus) < -(-tiles // cus):
+        pytest.skip(f"{cus} compute units: the thin row does not take the tiles down a round")
+    padded = mb + (17 - mb % 256 if mb % 256 <= 16 else 0)
+    assert padded % 256 > 16
+    g = torch.Generator().manual_seed(rank + mb + kb + nb)
+    a = torch.randn((rank, mb, kb), generator=g).to(dtype)
+    b = torch.randn((rank, nb, kb), generator=g).to(dtype)
+    a_padded = torch.cat([a, torch.zeros((rank, padded - mb, kb), dtype=dtype)], dim=1)
+
+    def device_operand(planes: torch.Tensor) -> torch.Tensor:
+        return torch.from_numpy(to_operand(planes.view(torch.int16).numpy())).to(DEVICE).view(dtype)
+
+    thin = torch.full((rank, mb, nb), float("nan"), device=DEVICE, dtype=product_dtype)
+    full = torch.full((rank, padded, nb), float("nan"), device=DEVICE, dtype=product_dtype)
+    _stages.leaf_products(rank, device_operand(a), device_operand(b), thin, mb, kb, nb)
+    _stages.leaf_products(rank, device_operand(a_padded), device_operand(b), full, padded, kb, nb)
+    torch.cuda.synchronize()
+    assert not torch.isnan(thin).any()
+    bits = torch.int32 if product_dtype == torch.float32 else torch.int16
+    assert torch.equal(thin.view(bits), full[:, :mb].contiguous().view(bits))
