@@ -122,7 +122,12 @@ int fastmm_leaf_scratch_bytes(int rank, int operand_dtype, int products_dtype, i
 /* Output recombination P[R, Mb, Nb] (products_dtype: fp16, bf16 or fp32) ->
  * output[rows, columns] in dtype, with an optional bias[columns] (NULL = none)
  * added in fp32 after the scheme's sum. Replaces _reconstruct / _reconstruct_bias + output_transform[_bias]_kernel
- * (runtime.py:657-698; rank7_2x2x2.py:207-345). */
+ * (runtime.py:657-698; rank7_2x2x2.py:207-345).
+ * The 8x8-block scheme with fp16 products, no bias and columns % 64 == 0 runs
+ * the reference's dense form instead (Rank343Plan._reconstruct,
+ * runtime.py:938-962: every output block as one fp32-accumulated MFMA
+ * contraction of the products with the scheme's -1/0/1 output matrix); its
+ * other inputs run the output circuit. */
 int fastmm_reconstruct(int scheme, int products_dtype, const void* products, const void* bias,
                        int dtype, void* output, int64_t rows, int64_t columns, void* stream);
 

@@ -1,6 +1,7 @@
 // Error channel and library identity of the C ABI.
 #include "abi_common.h"
 
+#include <atomic>
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -27,6 +28,19 @@ int check_launch(const char* what) {
 }
 
 void clear_error() { last_error[0] = '\0'; }
+
+// Compute units of the current device (cached per device; 0 if unknown).
+int compute_units() {
+  static std::atomic<int> cached[64];  // zero-initialized
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 0;
+  int units = cached[device].load(std::memory_order_relaxed);
+  if (units == 0) {
+    if (hipDeviceGetAttribute(&units, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return 0;
+    cached[device].store(units, std::memory_order_relaxed);
+  }
+  return units;
+}
 
 }  // namespace fastmm
 

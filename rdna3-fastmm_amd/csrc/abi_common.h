@@ -18,6 +18,9 @@ int check_launch(const char* what);
 // Clear the thread's last error at the start of an entry point.
 void clear_error();
 
+// Compute units of the current device (cached per device; 0 if unknown).
+int compute_units();
+
 inline bool aligned_to(const void* pointer, uintptr_t bytes) {
   return (reinterpret_cast<uintptr_t>(pointer) % bytes) == 0;
 }

@@ -1210,18 +1210,6 @@ __global__ __launch_bounds__(256) void tail_reduce_kernel(const float* __restric
   }
 }
 
-// Compute units of the current device (cached per device; 0 if unknown).
-int compute_units() {
-  static std::atomic<int> cached[64];  // zero-initialized
-  int device = 0;
-  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 0;
-  int units = cached[device].load(std::memory_order_relaxed);
-  if (units == 0) {
-    if (hipDeviceGetAttribute(&units, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return 0;
-    cached[device].store(units, std::memory_order_relaxed);
-  }
-  return units;
-}
 
 // One workgroup per CU: `total` tiles run in ceil(total / CUs) rounds, and a
 // last round of `tail` < CUs tiles leaves CUs idle for a whole tile time. The

@@ -11,6 +11,8 @@
 // every output with one vector store as soon as the program produces it.
 // Positions past the matrix read as zero (the reference's masked loads with
 // other=0.0). Programs come from csrc/generated/*.h.
+#include <algorithm>
+
 #include "abi_common.h"
 #include "fastmm_device.h"
 #include "generated/rank343_8x8x8.h"
@@ -276,6 +278,149 @@ __global__ __launch_bounds__(block_threads<S>()) void reconstruct_kernel(
   S::template output<Vec<EPT>>(load, store);
 }
 
+// ------------------------------------------- dense recombination (8x8 blocks)
+
+// The 8x8-block scheme's recombination as one dense contraction, the form the
+// reference runs (generated/rank343_8x8x8.py output_transform_mfma_kernel,
+// runtime.py:938-962): C block c = sum over r of M[c][r] * P[r], with fp16
+// products and coefficients (-1, 0, 1) multiplied on FP16 MFMA
+// (v_mfma_f32_16x16x32_f16), summed in fp32 and rounded once to the fp16
+// output. Every term is exact in fp32; only the fp32 summation order is the
+// hardware's. Rank-padded K runs over ceil(R / 32) steps of 32 products.
+//
+// One wave owns 64 plane positions per tile and all 64 outputs (4 x 4 MFMA
+// tiles of 16 positions x 16 outputs). Per K step it loads 32 products x 64
+// positions (a lane: 4 products x 8 positions, 16-byte loads), writes them
+// transposed into its own LDS stage (position-major, 32 products per row) and
+// reads the MFMA fragments back as 16-byte rows. The coefficient matrix sits
+// in LDS as fp16 for the whole kernel. Loads run kDepth K steps ahead.
+namespace dense {
+
+constexpr int kWaves = 4;
+constexpr int kPositions = 64;              // plane positions per wave and tile
+constexpr int kStep = 32;                   // products per MFMA K step
+constexpr int kStageRow = kStep * 2 + 16;   // bytes per staged position; the pad keeps the
+                                            // 16 rows a fragment read touches on distinct banks
+constexpr int kDepth = 6;                   // K steps of loads in flight per wave
+
+template <class S>
+constexpr int steps() { return (S::kRank + kStep - 1) / kStep; }
+// Bytes per output row of the staged matrix (padded like the stage rows).
+template <class S>
+constexpr int matrix_row() { return steps<S>() * kStep * 2 + 16; }
+template <class S>
+constexpr int lds_bytes() { return S::kSize * S::kSize * matrix_row<S>() + kWaves * kPositions * kStageRow; }
+
+__device__ __forceinline__ uint32_t component(const uint4& v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+// Requires cols == s * cols_b, cols_b % 8 == 0 (so plane % 8 == 0 and every
+// group of 8 positions lies in one plane row) and 16-byte aligned products.
+template <class S>
+__global__ __launch_bounds__(kWaves * 64) void dense_reconstruct_kernel(
+    const uint16_t* __restrict__ products, uint16_t* __restrict__ out, int64_t rows, int64_t cols,
+    int64_t rows_b, int64_t cols_b, int64_t tiles) {
+  constexpr int R = S::kRank, s = S::kSize, KS = steps<S>(), KP = KS * kStep;
+  constexpr int MROW = matrix_row<S>();
+  static_assert(s * s == 64, "four 16-output MFMA column blocks");
+  __shared__ __attribute__((aligned(16))) unsigned char lds[lds_bytes<S>()];
+  // M[c][r] as fp16 at c * MROW + 2 r, zero for r >= R
+  for (int i = threadIdx.x; i < s * s * KP; i += kWaves * 64) {
+    const int c = i / KP, r = i - c * KP;
+    const float m = r < R ? static_cast<float>(S::kOutputMatrix[c][r]) : 0.0f;
+    *reinterpret_cast<half_t*>(lds + c * MROW + 2 * r) = static_cast<half_t>(m);
+  }
+  __syncthreads();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  unsigned char* stage = lds + s * s * MROW + wave * kPositions * kStageRow;
+  const int64_t plane = rows_b * cols_b;
+  const int group = lane >> 3;               // loads products 4 group + j of each K step
+  const int span = lane & 7;                 // for tile positions 8 span .. 8 span + 7
+  const int fr = lane & 15, fk = lane >> 4;  // fragment row, 8-wide K chunk
+
+  for (int64_t tile = static_cast<int64_t>(blockIdx.x) * kWaves + wave; tile < tiles;
+       tile += static_cast<int64_t>(gridDim.x) * kWaves) {
+    const int64_t p0 = tile * kPositions;
+    const int64_t pos = p0 + 8 * span;
+    // Positions past the plane (plane % 8 == 0: whole groups) read position 0:
+    // a position's outputs depend on its own products only, and these are
+    // never stored. Products past R read product R - 1 and are zeroed (their
+    // coefficients are zero, but an Inf or NaN there would still poison the
+    // sum). Branch-free, so the loads pipeline.
+    const uint16_t* lane_products = products + (pos < plane ? pos : 0);
+    uint4 v[KS][4];
+    auto fetch = [&](int ks) __attribute__((always_inline)) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = ks * kStep + 4 * group + j;
+        v[ks][j] = *reinterpret_cast<const uint4*>(lane_products + static_cast<int64_t>(r < R ? r : R - 1) * plane);
+      }
+    };
+#pragma unroll
+    for (int ks = 0; ks < kDepth && ks < KS; ++ks) fetch(ks);
+    float4v acc[4][4];
+#pragma unroll
+    for (int pb = 0; pb < 4; ++pb)
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) acc[pb][cb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks + kDepth < KS) fetch(ks + kDepth);
+      uint32_t d[4][4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool keep = (ks + 1) * kStep <= R || ks * kStep + 4 * group + j < R;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) d[j][i] = keep ? component(v[ks][j], i) : 0u;
+      }
+      // position 8 span + q: products 4 group .. 4 group + 3 as one 8-byte row piece
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int i = q >> 1;
+        const uint32_t lo = (q & 1) ? (d[0][i] >> 16) | (d[1][i] & 0xffff0000u) : (d[0][i] & 0xffffu) | (d[1][i] << 16);
+        const uint32_t hi = (q & 1) ? (d[2][i] >> 16) | (d[3][i] & 0xffff0000u) : (d[2][i] & 0xffffu) | (d[3][i] << 16);
+        *reinterpret_cast<uint2*>(stage + (8 * span + q) * kStageRow + 8 * group) = make_uint2(lo, hi);
+      }
+      // A = P^T fragments (row: position 16 pb + fr), B = M^T fragments (column:
+      // output 16 cb + fr); lane l holds K values 8 fk .. 8 fk + 7 of its row.
+      uint4 a[4], b[4];
+#pragma unroll
+      for (int pb = 0; pb < 4; ++pb)
+        a[pb] = *reinterpret_cast<const uint4*>(stage + (16 * pb + fr) * kStageRow + 16 * fk);
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb)
+        b[cb] = *reinterpret_cast<const uint4*>(lds + (16 * cb + fr) * MROW + 2 * (ks * kStep + 8 * fk));
+#pragma unroll
+      for (int pb = 0; pb < 4; ++pb)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+          acc[pb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              __builtin_bit_cast(half8, a[pb]), __builtin_bit_cast(half8, b[cb]), acc[pb][cb], 0, 0, 0);
+    }
+    // Element e of acc[pb][cb] in lane l: output block 16 cb + fr at plane
+    // position p0 + 16 pb + 4 fk + e (four consecutive columns of one row).
+#pragma unroll
+    for (int pb = 0; pb < 4; ++pb) {
+      const int64_t p = p0 + 16 * pb + 4 * fk;
+      if (p >= plane) continue;
+      const int64_t row = p / cols_b, col = p - row * cols_b;
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) {
+        const int c = 16 * cb + fr;
+        const int64_t out_row = (c / s) * rows_b + row;
+        if (out_row >= rows) continue;
+        uint16_t h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = f32_to_fp16(acc[pb][cb][e]);
+        store16<4>(out + out_row * cols + (c % s) * cols_b + col, h);
+      }
+    }
+  }
+}
+
+}  // namespace dense
+
 // ------------------------------------------------------------- launchers
 
 template <class S>
@@ -422,6 +567,17 @@ int launch_reconstruct(int products_dtype, const void* products, const void* bia
     if (dtype != kFP16 || products_dtype == kBF16) {
       return fail(FASTMM_ERROR_UNSUPPORTED,
                   "reconstruct: the %dx%d-block scheme takes fp16 or fp32 products and an fp16 output", s, s);
+    }
+    // fp16 products, no bias, whole 8-column position groups: the dense MFMA
+    // form (the reference's); otherwise the output circuit below.
+    if (products_dtype == kFP16 && b == nullptr && cols == s * cols_b && cols_b % 8 == 0 &&
+        aligned_to(products, 16) && aligned_to(output, 8)) {
+      const int64_t tiles = ceil_div(plane, dense::kPositions);
+      const int64_t resident = 2 * static_cast<int64_t>(compute_units() > 0 ? compute_units() : 256);
+      const dim3 dense_grid(static_cast<unsigned>(std::min(ceil_div(tiles, dense::kWaves), resident)));
+      dense::dense_reconstruct_kernel<S><<<dense_grid, dense::kWaves * 64, 0, stream>>>(
+          static_cast<const uint16_t*>(products), out, rows, cols, rows_b, cols_b, tiles);
+      return check_launch("reconstruct");
     }
     if (products_dtype == kFP32) FASTMM_RECON(kFP32, kFP16);
     else FASTMM_RECON(kFP16, kFP16);

@@ -92,6 +92,30 @@ def emit_program(function: str, program: LinearProgram, comment: str) -> str:
     return "\n".join(lines)
 
 
+def emit_output_matrix(program: LinearProgram) -> str:
+    """The C-side map as a dense int8 matrix, ``kOutputMatrix[c][r]``.
+
+    Emitted for the 8x8-block scheme, whose recombination runs as one dense
+    MFMA contraction over the products, as in the reference
+    (``generated/rank343_8x8x8.py`` ``MFMA_OUTPUT_COEFFICIENTS``, written
+    rank-major there; here output-major, the layout the kernel stages). Every
+    coefficient must be an integer in [-128, 127].
+    """
+    rows = program.coefficients()
+    for row in rows:
+        for value in row:
+            if value.denominator != 1 or not -128 <= value.numerator <= 127:
+                raise ValueError("the dense output matrix needs int8 coefficients")
+    lines = [
+        f"// Output c = sum over r of kOutputMatrix[c][r] * P[r] ({program.output_count} x {program.input_count}).",
+        f"static constexpr signed char kOutputMatrix[{program.output_count}][{program.input_count}] = {{",
+    ]
+    for row in rows:
+        lines.append("    {" + ",".join(str(value.numerator) for value in row) + "},")
+    lines.append("};")
+    return "\n".join(lines)
+
+
 def _guard(scheme: Scheme) -> str:
     return f"FASTMM_GENERATED_{scheme.name.upper()}_H"
 
@@ -128,6 +152,7 @@ def emit_scheme_header(scheme: Scheme) -> str:
             "output", scheme.output,
             "Recombination: input r = product P[r]; output c = block (c / kSize, c % kSize) of C.",
         )),
+        *([ "", _indent(emit_output_matrix(scheme.output))] if scheme.size == 8 else []),
         "};",
         "",
         "}  // namespace fastmm",

@@ -58,6 +58,38 @@ def _fp16_only(scheme) -> bool:
     return scheme.size > 4
 
 
+def _dense_recombination(scheme, product_dtype, dtype, use_bias, n) -> bool:
+    """Inputs the library recombines with the 8x8-block scheme's dense MFMA form:
+    fp16 products, fp16 output, no bias and N a multiple of 64."""
+    return (scheme.size == 8 and product_dtype == torch.float16 and dtype == torch.float16
+            and not use_bias and n % 64 == 0)
+
+
+def _fp16_order(bits: np.ndarray) -> np.ndarray:
+    """fp16 bit patterns -> integers in value order (adjacent values differ by 1)."""
+    b = bits.astype(np.int32) & 0xFFFF
+    return np.where(b & 0x8000, -(b & 0x7FFF), b)
+
+
+def _assert_dense_match(out: torch.Tensor, oracle, products: np.ndarray, m: int, n: int) -> None:
+    """The dense form's result: the exact sum rounded once (oracle), up to the fp32
+    summation order, which is the MFMA's. Elementwise, |out - exact| is at most
+    one fp16 ulp of the output plus 343 fp32 units of the sum of |terms| (the
+    order's rounding; near cancellation that can exceed an fp16 ulp of a tiny
+    result). Almost every element is bit-exact."""
+    exact = O.reconstruct_dense(oracle, products, m, n, "fp32").astype(np.float64)
+    got_bits = _bits(out)
+    distance = np.abs(_fp16_order(got_bits) - _fp16_order(exact.astype(np.float16).view(np.int16)))
+    assert np.count_nonzero(distance) <= max(1, distance.size // 1000)
+    weights = np.abs(np.array(O.program_matrix(oracle.output), dtype=np.float64))  # [64, 343]
+    mb, nb = products.shape[1:]
+    magnitude = np.einsum("or,rmn->omn", weights, np.abs(products.astype(np.float64)))
+    magnitude = magnitude.reshape(8, 8, mb, nb).transpose(0, 2, 1, 3).reshape(8 * mb, 8 * nb)[:m, :n]
+    got = got_bits.view(np.float16)
+    ulp = np.spacing(np.abs(got)).astype(np.float64)
+    assert np.all(np.abs(got.astype(np.float64) - exact) <= ulp + 343 * 2.0**-24 * magnitude)
+
+
 def _plane_bits(planes: np.ndarray, plane_dtype: str) -> np.ndarray:
     if plane_dtype == "bf16":
         return O.round_to_bf16(planes).view(np.int16)
@@ -121,6 +153,9 @@ def test_reconstruct_bit_exact(key, shape, product_dtype) -> None:
             out = torch.empty((m, n), device=DEVICE, dtype=dtype)
             _stages.reconstruct(scheme, products.to(DEVICE), bias.to(DEVICE) if use_bias else None, out, m, n)
             torch.cuda.synchronize()
+            if _dense_recombination(scheme, product_dtype, dtype, use_bias, n):
+                _assert_dense_match(out, oracle, products.numpy(), m, n)
+                continue
             expected = O.reconstruct(
                 oracle,
                 products.numpy() if product_dtype == torch.float16 else products.float().numpy(),
@@ -130,6 +165,30 @@ def test_reconstruct_bit_exact(key, shape, product_dtype) -> None:
                 "bf16" if dtype == torch.bfloat16 else "fp16",
             )
             assert np.array_equal(_bits(out), expected.view(np.int16)), (dtype, use_bias)
+
+
+@pytest.mark.parametrize("shape", ((64, 64), (37, 128), (300, 192), (1000, 512), (2050, 1024)))
+def test_rank343_dense_recombination_matches_the_dense_oracle(shape) -> None:
+    """Rank 343, fp16 products and output, no bias: the dense MFMA contraction
+    (reference output_transform_mfma_kernel) against the oracle's dense form.
+    The shapes cover one and many tiles of 64 positions per wave, a partial last
+    tile (plane 2000 = 31.25 tiles at 1000 x 512), padded output rows
+    (M % 8 != 0) and small integers, which must come out exact."""
+    m, n = shape
+    print(f"\n[case] rank343 dense recombination {shape}", flush=True)
+    scheme = load_scheme("rank343")
+    oracle = O.load_oracle_scheme("rank343")
+    g = torch.Generator().manual_seed(m + 7 * n)
+    products = torch.randn((343, _ceil(m, 8), _ceil(n, 8)), generator=g).to(torch.float16)
+    out = torch.empty((m, n), device=DEVICE, dtype=torch.float16)
+    _stages.reconstruct(scheme, products.to(DEVICE), None, out, m, n)
+    torch.cuda.synchronize()
+    _assert_dense_match(out, oracle, products.numpy(), m, n)
+    integers = torch.randint(-3, 4, products.shape, generator=g).to(torch.float16)
+    _stages.reconstruct(scheme, integers.to(DEVICE), None, out, m, n)
+    torch.cuda.synchronize()
+    expected = O.reconstruct_dense(oracle, integers.numpy(), m, n, "fp16")
+    assert np.array_equal(_bits(out), expected.view(np.int16))
 
 
 @pytest.mark.parametrize(

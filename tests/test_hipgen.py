@@ -44,3 +44,22 @@ def test_emitted_programs_compute_the_certificate_maps() -> None:
                 got = _run_emitted(body, unit)
                 assert sorted(got) == list(range(program.output_count))
                 assert [got[k] for k in range(program.output_count)] == [row[column] for row in matrix]
+
+
+def test_dense_output_matrix_is_the_certificate_map() -> None:
+    """The 8x8-block scheme's kOutputMatrix (the dense recombination's operand)
+    equals the output program's exact coefficient matrix; only that scheme
+    carries one."""
+    for key in SCHEME_KEYS:
+        scheme = load_scheme(key)
+        header = hipgen.emit_scheme_header(scheme)
+        if scheme.size != 8:
+            assert "kOutputMatrix" not in header
+            continue
+        body = header[header.index("kOutputMatrix["):]
+        body = body[body.index("= {") + 3:body.index("};")]
+        rows = [[int(v) for v in row.split(",")] for row in re.findall(r"\{([-0-9,]+)\}", body)]
+        expected = scheme.output.coefficients()
+        assert len(rows) == scheme.size**2 == len(expected)
+        assert rows == [[int(v) for v in row] for row in expected]
+        assert all(v.denominator == 1 for row in expected for v in row)
