@@ -316,7 +316,8 @@ __device__ __forceinline__ uint32_t component(const uint4& v, int i) {
 }
 
 // Requires cols == s * cols_b, cols_b % 8 == 0 (so plane % 8 == 0 and every
-// group of 8 positions lies in one plane row) and 16-byte aligned products.
+// group of 8 positions lies in one plane row), 16-byte aligned products and an
+// 8-byte aligned output; the launcher checks all four.
 template <class S>
 __global__ __launch_bounds__(kWaves * 64) void dense_reconstruct_kernel(
     const uint16_t* __restrict__ products, uint16_t* __restrict__ out, int64_t rows, int64_t cols,
