@@ -574,7 +574,8 @@ int launch_reconstruct(int products_dtype, const void* products, const void* bia
     if (products_dtype == kFP16 && b == nullptr && cols == s * cols_b && cols_b % 8 == 0 &&
         aligned_to(products, 16) && aligned_to(output, 8)) {
       const int64_t tiles = ceil_div(plane, dense::kPositions);
-      const int64_t resident = 2 * static_cast<int64_t>(compute_units() > 0 ? compute_units() : 256);
+      const int cus = compute_units();  // two 4-wave workgroups fit a CU's LDS
+      const int64_t resident = 2 * static_cast<int64_t>(cus > 0 ? cus : 256);
       const dim3 dense_grid(static_cast<unsigned>(std::min(ceil_div(tiles, dense::kWaves), resident)));
       dense::dense_reconstruct_kernel<S><<<dense_grid, dense::kWaves * 64, 0, stream>>>(
           static_cast<const uint16_t*>(products), out, rows, cols, rows_b, cols_b, tiles);
