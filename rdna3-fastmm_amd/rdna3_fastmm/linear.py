@@ -12,8 +12,11 @@ library, which Inductor calls as a fallback kernel.
 ``rewrite_eligible_linears`` replaces eligible ``aten.linear`` nodes of a
 graph before AOT compilation, exactly where the reference does
 (linear.py:170-288): BF16 input/weight/bias on one GPU, contiguous, static
-shape, a measured-win family (rank-7 families first, then rank-49), and at
-most half of the free device memory for the temporaries.
+shape, a measured-win family, and at most half of the free device memory
+for the temporaries. The reference tries rank-7 families first, then rank-49
+(linear.py:240-252); here every scheme with measured MI355X families is a
+candidate (rank 7, rank 48, rank 49) and the one whose covering family was
+measured fastest is used, earlier schemes winning ties.
 """
 
 from typing import Callable, Optional
@@ -128,8 +131,27 @@ def _has_linear_memory_budget(plan_type: type, shape: tuple, device: torch.devic
     return allocation <= free_bytes * MAX_LINEAR_ALLOCATION_FREE_FRACTION
 
 
-# Dispatch order of the rewrite: the first plan with a measured win is used.
-_REWRITE_ORDER: tuple = ((Rank7Plan, RDNA3_RANK7_LINEAR_OP), (Rank49Plan, RDNA3_LINEAR_OP))
+# Candidate plans of the rewrite, in tie-break order: the plan whose covering
+# dynamic family was measured fastest is used (if its temporaries fit).
+_REWRITE_ORDER: tuple = (
+    (Rank7Plan, RDNA3_RANK7_LINEAR_OP),
+    (Rank48Plan, RDNA3_RANK48_LINEAR_OP),
+    (Rank49Plan, RDNA3_LINEAR_OP),
+)
+
+
+def _rewrite_choice(shape: tuple, has_bias: bool, device: torch.device) -> Optional[Callable]:
+    """The operator for the fastest measured dynamic family covering ``shape``, or None."""
+    ranked = []
+    for order, (plan_type, target) in enumerate(_REWRITE_ORDER):
+        plan: type[_LinearPlan] = plan_type
+        speedup = plan.measured_linear_speedup(shape, has_bias=has_bias)
+        if speedup is not None:
+            ranked.append((-speedup, order, plan, target))
+    if not ranked:
+        return None
+    _, _, plan, target = min(ranked, key=lambda item: item[:2])
+    return target if _has_linear_memory_budget(plan, shape, device) else None
 
 
 def _linear_node_target(node: Node) -> Optional[Callable]:
@@ -170,11 +192,7 @@ def _linear_node_target(node: Node) -> Optional[Callable]:
     elif bias_node is not None:
         return None
     shape = (input_tensor.numel() // inner, inner, columns)
-    for plan_type, target in _REWRITE_ORDER:
-        plan: type[_LinearPlan] = plan_type
-        if plan.has_measured_linear_win(shape, has_bias=has_bias):
-            return target if _has_linear_memory_budget(plan, shape, input_tensor.device) else None
-    return None
+    return _rewrite_choice(shape, has_bias, input_tensor.device)
 
 
 def rewrite_eligible_linears(graph_module: GraphModule, example_inputs: list) -> int:

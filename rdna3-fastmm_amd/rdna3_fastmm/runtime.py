@@ -24,7 +24,7 @@ Differences that are visible to a caller, all deliberate:
 
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 import json
 from pathlib import Path
 from typing import ClassVar
@@ -126,13 +126,19 @@ class PackedWeight(_PackedTransform):
 
 @dataclass(frozen=True)
 class LinearShapeFamily:
-    """Rows interval x exact (inner, columns) x bias, where a win was measured."""
+    """Rows interval x exact (inner, columns) x bias, where a win was measured.
+
+    ``measured_speedup`` is the smallest speedup over native measured inside the
+    family (0.0 when unknown, e.g. a family built by hand); it ranks plans when
+    families of several schemes cover one shape. It takes no part in equality.
+    """
 
     minimum_rows: int
     maximum_rows: int
     inner: int
     columns: int
     has_bias: bool
+    measured_speedup: float = field(default=0.0, compare=False)
 
     def matches(self, shape: tuple[int, int, int], has_bias: bool) -> bool:
         rows, inner, columns = shape
@@ -227,7 +233,7 @@ def load_dispatch_table(path: Path = DISPATCH_TABLE_PATH) -> dict[tuple[str, boo
         if not (0 < entry["minimum_rows"] <= entry["maximum_rows"]) or entry["minimum_speedup"] < document["minimum_speedup"]:
             raise ValueError(f"{path}: families[{index}] is not a measured win")
         family = LinearShapeFamily(entry["minimum_rows"], entry["maximum_rows"], entry["inner"], entry["columns"],
-                                   entry["bias"])
+                                   entry["bias"], float(entry["minimum_speedup"]))
         mode = "prepacked" if entry["prepacked"] else "dynamic"
         evidence = (f"{entry['scheme']} {mode}: >= {entry['minimum_speedup']}x native at {entry['points']} swept "
                     f"row counts, {entry['runs']} runs each")
@@ -584,6 +590,17 @@ class _LinearPlan(_Plan):
         if prepacked_weight:
             families += cls.prepacked_linear_shape_families
         return any(family.matches(tuple(shape), has_bias) for family in families)
+
+    @classmethod
+    def measured_linear_speedup(
+        cls, shape: tuple[int, int, int], *, has_bias: bool, prepacked_weight: bool = False
+    ) -> float | None:
+        """Largest measured speedup of the families covering ``shape`` (None: no win)."""
+        families = cls.linear_shape_families
+        if prepacked_weight:
+            families += cls.prepacked_linear_shape_families
+        speedups = [family.measured_speedup for family in families if family.matches(tuple(shape), has_bias)]
+        return max(speedups) if speedups else None
 
     def is_linear_recommended(self, *, has_bias: bool, prepacked_weight: bool = False) -> bool:
         return (

@@ -1,0 +1,244 @@
+"""Every BASELINE configuration at its full size, through the HIP library.
+
+The reference validates each benchmark run on a centred CPU-FP32 tile in every
+one of the s*s output macroblocks (benchmarks/benchmark.py:160-265) and tests
+its plans end to end on ragged shapes (tests/test_rdna3.py:433-613). Here each
+configuration (C1..C5 of the BASELINE file, the C5 controls, and the north
+star's rank-48 point at 8214 x 12288 x 4608) runs on its own seeded inputs
+(CPU generator: x ~ N(0,1), W ~ N(0,1/K), bias ~ N(0, 0.02), all BF16), and:
+
+* the transformed planes A' and B' are bit-exact against the oracle on a
+  sample of block rows / block columns (first, last, tile edges, padding rows,
+  random), computed by the oracle from just the input rows those planes read;
+* the leaf products on that row x column sample stay within the fp32
+  accumulation bound of the oracle's near-exact sums (plus one fp16 rounding);
+* the output at those positions, in every output macroblock, is bit-equal to
+  the oracle's recombination (+ bias, one BF16 rounding) of the GPU's own
+  products;
+* the dynamic and the prepacked plan agree bitwise over the whole output, the
+  packed weight equals the dynamic B', and a reused output buffer gives the
+  same bits again;
+* no value is non-finite, and the full-output relative L2 error against an
+  fp64 product is at most 1.2x native BF16 F.linear's (rank 49: inside the
+  band its fp16 operand rounding puts it in, above the bound, as the oracle
+  predicts);
+* the reference's per-macroblock centred tiles against a CPU fp32 product
+  stay below its rel-L2 5e-3 bound.
+
+C1 (1024^3, rank 7) is small enough to check against the oracle's whole
+evaluation.
+"""
+
+from __future__ import annotations
+
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fastmm_oracle as O
+from rdna3_fastmm.runtime import PLAN_TYPES
+
+pytestmark = pytest.mark.gpu
+DEVICE = torch.device("cuda", 0)
+TILE = 16  # centred tile per output macroblock (the reference uses 8..32)
+
+# id: (scheme, rows, inner, columns, bias)
+CONFIGS = {
+    "C1-rank7-1024": ("rank7", 1024, 1024, 1024, False),
+    "C2-rank7-4096x4096x12288": ("rank7", 4096, 4096, 12288, False),
+    "C3-rank7-8214x12288x4608-bias": ("rank7", 8214, 12288, 4608, True),
+    "C4-rank49-19968x4096x16384-bias": ("rank49", 19968, 4096, 16384, True),
+    "C5-rank48-8192": ("rank48", 8192, 8192, 8192, False),
+    "C5-control-rank7-8192": ("rank7", 8192, 8192, 8192, False),
+    "C5-control-rank49-8192": ("rank49", 8192, 8192, 8192, False),
+    "target-rank48-8214x12288x4608": ("rank48", 8214, 12288, 4608, False),
+}
+# Rank 49's fp16 planes alone cost ~1.4x native BF16's error (the oracle's
+# prediction; measured 1.67x with fp16 products), beyond the 1.2x bound.
+RANK49_BAND = (1.2, 1.9)
+ERROR_RATIO_BOUND = 1.2
+
+
+def baseline_inputs(rows: int, inner: int, columns: int, bias: bool, seed: int = 0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((rows, inner), generator=g).to(torch.bfloat16)
+    w = (torch.randn((columns, inner), generator=g) / inner**0.5).to(torch.bfloat16)
+    b = (torch.randn((columns,), generator=g) * 0.02).to(torch.bfloat16) if bias else None
+    return x, w, b
+
+
+def sample_block_indices(size: int, count: int, rng: np.random.Generator, extent: int, s: int) -> np.ndarray:
+    """First and last block rows, the last valid row of each of the s blocks of a
+    dimension of ``extent`` (ragged edges), the leaf GEMM's tile edges, and random ones."""
+    chosen = {0, 1, size // 2, size - 2, size - 1}
+    chosen |= {min(size, extent - i * size) - 1 for i in range(s) if extent > i * size}
+    chosen |= {v for v in (15, 16, 255, 256, 257, (size // 256) * 256) if 0 <= v < size}
+    chosen |= set(rng.choice(size, size=min(count, size), replace=False).tolist())
+    return np.array(sorted(chosen), dtype=np.int64)
+
+
+def source_rows(source: torch.Tensor, s: int, block: int, index: np.ndarray):
+    """Rows i*block + index of ``source`` for i < s, zero past its end (fp32).
+
+    Transforming this [s*len(index), K] matrix gives exactly the planes' rows
+    ``index`` (block i of the sub-matrix holds block i's sampled rows)."""
+    rows = (np.arange(s)[:, None] * block + index[None, :]).reshape(-1)
+    valid = rows < source.shape[0]
+    out = np.zeros((rows.size, source.shape[1]), dtype=np.float32)
+    out[valid] = source[torch.from_numpy(rows[valid])].float().numpy()
+    return out, rows, valid
+
+
+def gather_plane_rows(buffer: torch.Tensor, rank: int, rows: int, inner: int, index: np.ndarray) -> np.ndarray:
+    """Plane rows ``index`` of an operand buffer (either layout) as int16 bits [R, n, inner]."""
+    at = torch.from_numpy(index).to(buffer.device)
+    if inner % 32 == 0:
+        view = buffer.view(rank, inner // 32, rows, 32)[:, :, at, :].permute(0, 2, 1, 3).reshape(rank, -1, inner)
+    else:
+        view = buffer.view(rank, rows, inner)[:, at, :]
+    return view.contiguous().view(torch.int16).cpu().numpy()
+
+
+def rel_l2(candidate: torch.Tensor, exact: torch.Tensor) -> float:
+    return float(torch.linalg.vector_norm(candidate.double() - exact) / torch.linalg.vector_norm(exact))
+
+
+def check_sampled_stages(plan, scheme, x, w, b, workspace, output, rng) -> None:
+    """A'/B' bits, products within bound and output bits on a block-row x block-column sample."""
+    s, rank = plan.scheme_size, plan.rank
+    shape = plan.shape
+    mb, kb, nb = shape.block_rows, shape.block_inner, shape.block_columns
+    ri = sample_block_indices(mb, 12, rng, shape.rows, s)
+    ci = sample_block_indices(nb, 12, rng, shape.columns, s)
+    x_sub, out_rows, row_ok = source_rows(x, s, mb, ri)
+    w_sub, out_cols, col_ok = source_rows(w, s, nb, ci)
+    a = O.left_transform(scheme, x_sub)
+    bt = O.weight_transform(scheme, w_sub)
+    assert a.shape == (rank, ri.size, kb) and bt.shape == (rank, ci.size, kb)
+    left_bits = gather_plane_rows(workspace.left_transformed, rank, mb, kb, ri)
+    right_bits = gather_plane_rows(workspace.right_transformed, rank, nb, kb, ci)
+    assert np.array_equal(left_bits, a.view(np.int16)), "A' differs from the oracle"
+    assert np.array_equal(right_bits, bt.view(np.int16)), "B' differs from the oracle"
+
+    at_r, at_c = torch.from_numpy(ri).to(DEVICE), torch.from_numpy(ci).to(DEVICE)
+    products = workspace.products[:, at_r][:, :, at_c].cpu().numpy()
+    exact = O.leaf_products(a, bt, product_dtype="fp32").astype(np.float64)
+    magnitude = np.matmul(np.abs(a.astype(np.float64)), np.abs(np.swapaxes(bt.astype(np.float64), 1, 2)))
+    bound = kb * 2.0**-24 * magnitude + np.abs(exact) * 2.0**-11 + 2.0**-24
+    assert np.all(np.abs(products.astype(np.float64) - exact) <= bound), "leaf products outside the bound"
+
+    bias_sub = None
+    if b is not None:
+        bias_sub = np.zeros(out_cols.size, dtype=np.float32)
+        bias_sub[col_ok] = b[torch.from_numpy(out_cols[col_ok])].float().numpy()
+    recombined = O.reconstruct(scheme, products, out_rows.size, out_cols.size, bias_sub, "bf16")
+    gpu_rows = torch.from_numpy(out_rows[row_ok]).to(DEVICE)
+    gpu_cols = torch.from_numpy(out_cols[col_ok]).to(DEVICE)
+    got = output[gpu_rows][:, gpu_cols].view(torch.int16).cpu().numpy()
+    want = recombined[row_ok][:, col_ok].view(np.int16)
+    assert np.array_equal(got, want), "output differs from the oracle's recombination of the GPU's products"
+
+
+def macroblock_tile_errors(plan, x, w, b, output) -> list[float]:
+    """reference benchmark.py:160-265: a centred tile per macroblock vs CPU fp32."""
+    s = plan.scheme_size
+    m, k, n = plan.shape.dimensions
+    errors = []
+    for br in range(s):
+        r0 = br * plan.shape.block_rows
+        r1 = min(r0 + plan.shape.block_rows, m)
+        rs = r0 + (r1 - r0 - TILE) // 2
+        for bc in range(s):
+            c0 = bc * plan.shape.block_columns
+            c1 = min(c0 + plan.shape.block_columns, n)
+            cs = c0 + (c1 - c0 - TILE) // 2
+            reference = x[rs:rs + TILE].float() @ w[cs:cs + TILE].float().T
+            if b is not None:
+                reference += b[cs:cs + TILE].float()
+            candidate = output[rs:rs + TILE, cs:cs + TILE].float().cpu()
+            assert torch.isfinite(candidate).all()
+            errors.append(float(torch.linalg.vector_norm(candidate - reference) / torch.linalg.vector_norm(reference)))
+    return errors
+
+
+@pytest.mark.parametrize("config", list(CONFIGS))
+def test_baseline_config_through_the_hip_path(config: str) -> None:
+    key, m, k, n, has_bias = CONFIGS[config]
+    print(f"\n[case] {config}: {key} {m}x{k}x{n} bias={has_bias}", flush=True)
+    torch.cuda.empty_cache()
+    rng = np.random.default_rng(zlib.crc32(config.encode()))
+    x_cpu, w_cpu, b_cpu = baseline_inputs(m, k, n, has_bias)
+    x, w = x_cpu.to(DEVICE), w_cpu.to(DEVICE)
+    b = None if b_cpu is None else b_cpu.to(DEVICE)
+    plan = PLAN_TYPES[key](m, k, n, DEVICE, dtype=torch.bfloat16, compute_dtype=torch.float16)
+    scheme = O.load_oracle_scheme(key)
+
+    workspace = plan.allocate_workspace()
+    dynamic = plan.run_linear(x, w, workspace, b)  # output allocated per call
+    torch.cuda.synchronize()
+    check_sampled_stages(plan, scheme, x_cpu, w_cpu, b_cpu, workspace, dynamic, rng)
+
+    packed = plan.pack_weight(w)
+    assert torch.equal(packed.transformed, workspace.right_transformed)
+    packed_workspace = plan.allocate_workspace(prepacked_right=True)
+    out = torch.empty((m, n), device=DEVICE, dtype=torch.bfloat16)
+    first = plan.run_linear_packed(x, packed, packed_workspace, b, out)
+    assert first.data_ptr() == out.data_ptr()
+    assert torch.equal(first, dynamic), "prepacked output differs from the dynamic one"
+    snapshot = first.clone()
+    assert torch.equal(plan.run_linear_packed(x, packed, packed_workspace, b, out), snapshot)
+    del packed_workspace, snapshot, first
+
+    assert int((~torch.isfinite(dynamic)).sum()) == 0
+    exact = x.double() @ w.double().T
+    if b is not None:
+        exact += b.double()
+    native = rel_l2(torch.nn.functional.linear(x, w, b), exact)
+    ratio = rel_l2(dynamic, exact) / native
+    del exact
+    tiles = macroblock_tile_errors(plan, x_cpu, w_cpu, b_cpu, dynamic)
+    print(f"[ratio] {config}: native rel-L2 {native:.3e}, error ratio {ratio:.4f}, "
+          f"macroblock tiles max rel-L2 {max(tiles):.2e}", flush=True)
+    assert max(tiles) < 5e-3
+    if key == "rank49":
+        assert RANK49_BAND[0] < ratio < RANK49_BAND[1]
+    else:
+        assert ratio <= ERROR_RATIO_BOUND
+
+
+def test_c1_matches_the_whole_oracle_evaluation() -> None:
+    """C1 (rank 7, 1024^3): every plane bit-exact, every product within the bound,
+    the output bit-equal to the oracle's recombination of the GPU's products and
+    within one product rounding of the oracle's own end-to-end evaluation."""
+    print("\n[case] C1 full oracle 1024^3", flush=True)
+    m = k = n = 1024
+    x_cpu, w_cpu, _ = baseline_inputs(m, k, n, False)
+    plan = PLAN_TYPES["rank7"](m, k, n, DEVICE, dtype=torch.bfloat16, compute_dtype=torch.float16)
+    workspace = plan.allocate_workspace()
+    out = plan.run_linear(x_cpu.to(DEVICE), w_cpu.to(DEVICE), workspace).cpu()
+    scheme = O.load_oracle_scheme("rank7")
+    xn, wn = x_cpu.float().numpy(), w_cpu.float().numpy()
+    a = O.left_transform(scheme, xn)
+    bt = O.weight_transform(scheme, wn)
+    rank, mb, kb = a.shape
+    nb = bt.shape[1]
+    everything = np.arange(mb)
+    assert np.array_equal(gather_plane_rows(workspace.left_transformed, rank, mb, kb, everything), a.view(np.int16))
+    assert np.array_equal(gather_plane_rows(workspace.right_transformed, rank, nb, kb, np.arange(nb)),
+                          bt.view(np.int16))
+    products = workspace.products.cpu().numpy()
+    exact = O.leaf_products(a, bt, product_dtype="fp32").astype(np.float64)
+    magnitude = np.matmul(np.abs(a.astype(np.float64)), np.abs(np.swapaxes(bt.astype(np.float64), 1, 2)))
+    bound = kb * 2.0**-24 * magnitude + np.abs(exact) * 2.0**-11 + 2.0**-24
+    assert np.all(np.abs(products.astype(np.float64) - exact) <= bound)
+    assert np.array_equal(out.view(torch.int16).numpy(), O.reconstruct(scheme, products, m, n).view(np.int16))
+    # the oracle's own evaluation (near-exact leaf sums): products may differ by one
+    # fp16 rounding where the fp32 sum sits at a rounding boundary
+    whole = O.bf16_bits_to_f32(O.linear(scheme, xn, wn))
+    got = out.float().numpy()
+    reference = xn.astype(np.float64) @ wn.astype(np.float64).T
+    oracle_error = np.linalg.norm(whole - reference)
+    assert np.linalg.norm(got - whole) <= 0.1 * oracle_error
+    assert np.mean(got != whole) < 0.01

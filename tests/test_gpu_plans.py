@@ -217,6 +217,64 @@ def test_linear_ops_support_leading_dimensions(op) -> None:
     assert _rel(candidate, reference) < 0.005
 
 
+# Allocating operator -> scheme key, and one shape per scheme whose leaf GEMM
+# runs the split-K tail (every 256 x 256 tile in the last partial round, split
+# in 2-3 K parts: rank 7 56 tiles, rank 48 96 tiles, rank 49 49 tiles).
+OPERATOR_SCHEMES = (("linear_rank7", "rank7"), ("linear_rank48", "rank48"), ("linear", "rank49"))
+SPLIT_TAIL_SHAPES = {"rank7": (2048, 1024, 1024), "rank48": (2048, 1024, 1024), "rank49": (1024, 1024, 1024)}
+
+
+@pytest.mark.parametrize("op_name, key", OPERATOR_SCHEMES)
+@pytest.mark.parametrize("case", ("ragged", "split_tail", "no_bias"))
+def test_linear_ops_equal_the_plan_bitwise(op_name, key, case) -> None:
+    """The allocating operators (own buffers, early frees, own split-K scratch) give
+    exactly the plan's run_linear bits: leading dimensions, bias, a ragged shape and
+    a shape whose leaf GEMM runs the split-K tail. reference linear.py:50-167,
+    tests/test_rdna3.py:680-709."""
+    from rdna3_fastmm import _stages
+
+    if case == "ragged":
+        lead, (k, n) = (2, 17), (19, 23)
+    else:
+        m, k, n = SPLIT_TAIL_SHAPES[key]
+        lead = (2, m // 2)
+    print(f"\n[case] op {op_name} {case} lead={lead} K={k} N={n}", flush=True)
+    g = torch.Generator().manual_seed(53)
+    x = torch.randn((*lead, k), generator=g).to(torch.bfloat16).to(DEVICE)
+    w = (torch.randn((n, k), generator=g) / k**0.5).to(torch.bfloat16).to(DEVICE)
+    b = None if case == "no_bias" else (torch.randn((n,), generator=g) * 0.02).to(torch.bfloat16).to(DEVICE)
+    rows = x.numel() // k
+    plan = PLAN_TYPES[key](rows, k, n, DEVICE, dtype=torch.bfloat16, compute_dtype=torch.float16)
+    if case != "ragged":
+        shape = plan.shape
+        assert _stages.leaf_scratch_bytes(plan.rank, torch.float16, torch.float16, shape.block_rows,
+                                          shape.block_inner, shape.block_columns, DEVICE) > 0
+    candidate = getattr(torch.ops.rdna3_fastmm, op_name)(x, w, b)
+    assert candidate.shape == (*lead, n) and candidate.dtype == torch.bfloat16
+    workspace = plan.allocate_workspace(max_free_memory_fraction=0.1)
+    expected = plan.run_linear(x.reshape(rows, k), w, workspace, b)
+    assert torch.equal(candidate.reshape(rows, n), expected)
+    if case != "ragged":
+        return
+    # at the ragged shape the plan's stages (hence the operator's output) against the oracle
+    torch.cuda.synchronize()
+    oracle = O.load_oracle_scheme(key)
+    xn, wn = x.reshape(rows, k).float().cpu().numpy(), w.float().cpu().numpy()
+    a, bt = O.left_transform(oracle, xn), O.weight_transform(oracle, wn)
+    rank, mb, kb = a.shape
+    assert np.array_equal(from_operand(workspace.left_transformed.cpu().numpy().view(np.int16), rank, mb, kb),
+                          a.view(np.int16))
+    assert np.array_equal(from_operand(workspace.right_transformed.cpu().numpy().view(np.int16), rank,
+                                       bt.shape[1], kb), bt.view(np.int16))
+    products = workspace.products.cpu().numpy()
+    exact = O.leaf_products(a, bt, product_dtype="fp32").astype(np.float64)
+    magnitude = np.matmul(np.abs(a.astype(np.float64)), np.abs(np.swapaxes(bt.astype(np.float64), 1, 2)))
+    assert np.all(np.abs(products.astype(np.float64) - exact)
+                  <= kb * 2.0**-24 * magnitude + np.abs(exact) * 2.0**-11 + 2.0**-24)
+    recombined = O.reconstruct(oracle, products, rows, n, b.float().cpu().numpy(), "bf16")
+    assert np.array_equal(candidate.reshape(rows, n).cpu().view(torch.int16).numpy(), recombined.view(np.int16))
+
+
 @pytest.mark.parametrize("key", ("rank7", "rank48", "rank49"))
 def test_error_ratio_against_native_bf16(key) -> None:
     """North-star tolerance at a moderate shape: candidate <= 1.2x native BF16 error.
@@ -266,6 +324,35 @@ def test_rewritten_graph_runs_a_measured_family() -> None:
     exact = x.double() @ w.double().T
     ratio = _rel(out, exact) / _rel(torch.nn.functional.linear(x, w), exact)
     print(f"[ratio] rewritten rank7 {ratio:.3f}", flush=True)
+    assert ratio <= 1.2
+
+
+def test_rewritten_graph_runs_a_rank48_family(monkeypatch) -> None:
+    """Llama-3-70B's 28672 -> 8192 down projection at 13952 rows is covered only by a
+    rank-48 dynamic family of the shipped table: the rewritten graph runs
+    linear_rank48, bit-equal to Rank48Plan.run_linear and within the error bound."""
+    from rdna3_fastmm.linear import RDNA3_RANK48_LINEAR_OP, rewrite_eligible_linears
+
+    class Down(torch.nn.Module):
+        def forward(self, input_tensor, weight):
+            return torch.nn.functional.linear(input_tensor, weight)
+
+    m, k, n = 13952, 28672, 8192
+    print(f"\n[case] rewritten graph, {m}x{k} -> {n} (rank 48)", flush=True)
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn((m, k), generator=g).to(torch.bfloat16).to(DEVICE)
+    w = (torch.randn((n, k), generator=g) / k**0.5).to(torch.bfloat16).to(DEVICE)
+    gm = torch.fx.symbolic_trace(Down())
+    for node, tensor in zip((node for node in gm.graph.nodes if node.op == "placeholder"), (x, w)):
+        node.meta["val"] = tensor
+    assert rewrite_eligible_linears(gm, [x, w]) == 1
+    assert RDNA3_RANK48_LINEAR_OP in {node.target for node in gm.graph.nodes if node.op == "call_function"}
+    out = gm(x, w)
+    plan = Rank48Plan(m, k, n, DEVICE, dtype=torch.bfloat16, compute_dtype=torch.float16)
+    assert torch.equal(out, plan.run_linear(x, w, plan.allocate_workspace()))
+    exact = x.double() @ w.double().T
+    ratio = _rel(out, exact) / _rel(torch.nn.functional.linear(x, w), exact)
+    print(f"[ratio] rewritten rank48 {ratio:.3f}", flush=True)
     assert ratio <= 1.2
 
 

@@ -14,10 +14,11 @@ from rdna3_fastmm import external_mm, inductor, linear
 from rdna3_fastmm.linear import (
     RDNA3_LINEAR_OP,
     RDNA3_RANK7_LINEAR_OP,
+    RDNA3_RANK48_LINEAR_OP,
     _linear_node_target,
     rewrite_eligible_linears,
 )
-from rdna3_fastmm.runtime import LinearShapeFamily, Rank7Plan, Rank49Plan
+from rdna3_fastmm.runtime import LinearShapeFamily, Rank7Plan, Rank48Plan, Rank49Plan
 
 
 class Linear(torch.nn.Module):
@@ -119,6 +120,51 @@ def test_shipped_tables_rewrite_a_measured_down_projection(monkeypatch) -> None:
     gm = traced(Linear(), x, w)
     assert rewrite_eligible_linears(gm, [x, w]) == 1
     assert RDNA3_RANK7_LINEAR_OP in targets(gm)
+
+
+def test_shipped_tables_rewrite_a_rank48_only_family(monkeypatch) -> None:
+    """Llama-3-70B's 28672 -> 8192 down projection at 13952 rows: only a rank-48
+    dynamic family covers it in the shipped MI355X table."""
+    monkeypatch.setattr(torch.cuda, "mem_get_info", lambda device=None: (200 << 30, 288 << 30))
+    shape = (13_952, 28_672, 8_192)
+    assert Rank48Plan.has_measured_linear_win(shape, has_bias=False)
+    assert not Rank7Plan.has_measured_linear_win(shape, has_bias=False)
+    (x, w), _ = fake(shape[:2], (shape[2], shape[1]))
+    gm = traced(Linear(), x, w)
+    assert rewrite_eligible_linears(gm, [x, w]) == 1
+    assert RDNA3_RANK48_LINEAR_OP in targets(gm)
+
+
+def test_shipped_tables_prefer_the_faster_family(monkeypatch) -> None:
+    """12288 -> 4096 at 6272 rows is covered by a rank-7 and a rank-48 dynamic
+    family; the rank-48 one was measured faster there, so the rewrite picks it."""
+    monkeypatch.setattr(torch.cuda, "mem_get_info", lambda device=None: (200 << 30, 288 << 30))
+    shape = (6_272, 12_288, 4_096)
+    r7 = Rank7Plan.measured_linear_speedup(shape, has_bias=False)
+    r48 = Rank48Plan.measured_linear_speedup(shape, has_bias=False)
+    assert r7 is not None and r48 is not None and r48 > r7
+    (x, w), _ = fake(shape[:2], (shape[2], shape[1]))
+    gm = traced(Linear(), x, w)
+    assert rewrite_eligible_linears(gm, [x, w]) == 1
+    assert RDNA3_RANK48_LINEAR_OP in targets(gm)
+
+
+def test_rewrite_ranks_plans_by_measured_speedup(monkeypatch) -> None:
+    """Overlapping families: the faster one wins; equal speedups keep rank 7 first;
+    the chosen plan's memory budget still applies."""
+    monkeypatch.setattr(torch.cuda, "mem_get_info", lambda device=None: (200 << 30, 288 << 30))
+    (x, w), _ = fake((5120, 4608), (12288, 4608))
+    for r7, r48, expected in ((1.10, 1.30, RDNA3_RANK48_LINEAR_OP), (1.30, 1.10, RDNA3_RANK7_LINEAR_OP),
+                              (1.20, 1.20, RDNA3_RANK7_LINEAR_OP)):
+        monkeypatch.setattr(Rank7Plan, "linear_shape_families",
+                            (LinearShapeFamily(4_096, 6_144, 4_608, 12_288, False, r7),))
+        monkeypatch.setattr(Rank48Plan, "linear_shape_families",
+                            (LinearShapeFamily(5_000, 5_200, 4_608, 12_288, False, r48),))
+        gm = traced(Linear(), x, w)
+        assert rewrite_eligible_linears(gm, [x, w]) == 1
+        assert expected in targets(gm)
+    # the speedup takes no part in a family's identity
+    assert LinearShapeFamily(1, 2, 3, 4, False, 1.5) == LinearShapeFamily(1, 2, 3, 4, False)
 
 
 def test_operators_are_registered_with_fake_kernels() -> None:

@@ -272,3 +272,24 @@ def test_error_ratio_prediction() -> None:
         ratios[key] = np.linalg.norm(out - exact) / norm / native
     assert ratios["rank7"] < 1.2 and ratios["rank48"] < 1.2
     assert ratios["rank49"] > 1.2
+
+
+def test_c1_cpu_scheme_path_meets_the_error_bound() -> None:
+    """BASELINE C1: rank 7 at 1024^3 through the CPU scheme evaluation (the path
+    bench.py's cpu_c1 times), on the BASELINE inputs (seeded CPU torch.Generator,
+    x ~ N(0,1), W ~ N(0,1/K), BF16): rel-L2 against an fp64 product within 1.2x
+    of native BF16's (fp32 sum of the bf16 inputs, rounded once to bf16), with
+    fp32 (BLAS) and near-exact leaf sums alike, and no non-finite values."""
+    import torch
+
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn((1024, 1024), generator=g).to(torch.bfloat16).float().numpy()
+    w = (torch.randn((1024, 1024), generator=g) / 1024**0.5).to(torch.bfloat16).float().numpy()
+    exact = x.astype(np.float64) @ w.T.astype(np.float64)
+    norm = np.linalg.norm(exact)
+    native = np.linalg.norm(O.bf16_bits_to_f32(O.round_to_bf16(x @ w.T)) - exact) / norm
+    scheme = O.load_oracle_scheme("rank7")
+    for accumulate in ("f32", "f64"):
+        out = O.bf16_bits_to_f32(O.linear(scheme, x, w, accumulate=accumulate))
+        assert np.isfinite(out).all()
+        assert np.linalg.norm(out - exact) / norm <= 1.2 * native
