@@ -113,6 +113,23 @@ int fastmm_leaf_products(int rank, int operand_dtype, const void* left_transform
                          int64_t block_rows, int64_t block_inner, int64_t block_columns,
                          void* scratch, int64_t scratch_bytes, void* stream);
 
+/* fastmm_leaf_products without caller scratch and without any allocation: the
+ * split-K tail's fp32 parts go to a device array that the library holds
+ * (FASTMM_STATIC_SCRATCH_BYTES = 48 MiB, one copy per GPU the library runs
+ * on, kept until the process ends), so the results are the same bits as
+ * fastmm_leaf_products given enough scratch. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). It calls no
+ * hipMalloc/hipFree. Shapes whose tail would need more than the array return
+ * FASTMM_ERROR_UNSUPPORTED (on a 256-CU MI355X the tail never needs more).
+ * Every call on one GPU shares that GPU's array: calls that overlap in time
+ * on one GPU (other streams, other host threads) race and must not be issued;
+ * calls on one stream are ordered and safe. */
+#define FASTMM_STATIC_SCRATCH_BYTES (48LL << 20)
+int fastmm_leaf_products_noalloc(int rank, int operand_dtype, const void* left_transformed,
+                                 const void* right_transformed, void* products, int products_dtype,
+                                 int64_t block_rows, int64_t block_inner, int64_t block_columns, void* stream);
+
 /* Scratch bytes fastmm_leaf_products can use for these arguments on the
  * current device (0 when the shape runs no split-K tail). No counterpart in
  * the reference (torch.bmm manages its own workspace). */

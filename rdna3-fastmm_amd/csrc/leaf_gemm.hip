@@ -46,6 +46,7 @@
 // shapes where the fast kernel's preconditions fail.
 #include <algorithm>
 #include <atomic>
+#include <mutex>
 
 #include "abi_common.h"
 #include "fastmm_device.h"
@@ -1441,20 +1442,15 @@ int launch_leaf_products(const void* a, const void* b, void* p, int64_t rank, in
 
 }  // namespace fastmm
 
-extern "C" int fastmm_leaf_products(int rank, int operand_dtype, const void* left_transformed,
-                                    const void* right_transformed, void* products,
-                                    int products_dtype, int64_t block_rows, int64_t block_inner,
-                                    int64_t block_columns, void* scratch, int64_t scratch_bytes,
-                                    void* stream) {
-  clear_error();
-  if (scratch_bytes < 0 || (scratch == nullptr && scratch_bytes != 0)) {
-    return fail(FASTMM_ERROR_ARGUMENT, "leaf products: scratch of %lld bytes at null",
-                static_cast<long long>(scratch_bytes));
-  }
-  if (left_transformed == nullptr || right_transformed == nullptr || products == nullptr) {
+namespace fastmm {
+
+// Argument checks shared by both leaf-product entry points; FASTMM_OK or the error.
+int check_leaf_arguments(int rank, int operand_dtype, const void* a, const void* b, const void* p,
+                         int products_dtype, int64_t mb, int64_t kb, int64_t nb) {
+  if (a == nullptr || b == nullptr || p == nullptr) {
     return fail(FASTMM_ERROR_ARGUMENT, "leaf products: null pointer");
   }
-  if (rank < 1 || block_rows < 1 || block_inner < 1 || block_columns < 1) {
+  if (rank < 1 || mb < 1 || kb < 1 || nb < 1) {
     return fail(FASTMM_ERROR_ARGUMENT, "leaf products: dimensions must be positive");
   }
   if (operand_dtype != kFP16 && operand_dtype != kBF16) {
@@ -1465,23 +1461,120 @@ extern "C" int fastmm_leaf_products(int rank, int operand_dtype, const void* lef
                 "leaf products: products must be fp32 or the operands' type (%d), got %d",
                 operand_dtype, products_dtype);
   }
-  if (block_rows * block_inner > INT32_MAX || block_columns * block_inner > INT32_MAX ||
-      block_rows * block_columns > INT32_MAX) {
+  if (mb * kb > INT32_MAX || nb * kb > INT32_MAX || mb * nb > INT32_MAX) {
     return fail(FASTMM_ERROR_UNSUPPORTED, "leaf products: plane larger than 2^31 elements");
   }
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  const void* a = left_transformed;
-  const void* b = right_transformed;
-  void* p = products;
-  const int64_t mb = block_rows, kb = block_inner, nb = block_columns;
-  void* w = scratch;
-  const int64_t wb = scratch_bytes;
+  return FASTMM_OK;
+}
+
+// Element-type dispatch of checked arguments.
+int run_leaf_products(int rank, int operand_dtype, const void* a, const void* b, void* p, int products_dtype,
+                      int64_t mb, int64_t kb, int64_t nb, void* w, int64_t wb, hipStream_t s) {
   if (operand_dtype == kBF16) {
     if (products_dtype == kFP32) return launch_leaf_products<kBF16, kFP32>(a, b, p, rank, mb, kb, nb, w, wb, s);
     return launch_leaf_products<kBF16, kBF16>(a, b, p, rank, mb, kb, nb, w, wb, s);
   }
   if (products_dtype == kFP32) return launch_leaf_products<kFP16, kFP32>(a, b, p, rank, mb, kb, nb, w, wb, s);
   return launch_leaf_products<kFP16, kFP16>(a, b, p, rank, mb, kb, nb, w, wb, s);
+}
+
+// Split-K scratch bytes the 16x16x32 path plans for these arguments (0: no
+// split tail), assuming 16-byte aligned buffers; the launcher re-checks the
+// real pointers and runs the tail as whole tiles when they do not qualify.
+int64_t planned_scratch_bytes(int rank, int products_dtype, int64_t mb, int64_t kb, int64_t nb) {
+  const int64_t out_align = products_dtype == kFP32 ? 4 : 8;
+  if (kb % fast::BK != 0 || kb < 3 * fast::BK || nb % out_align != 0 || !mfma16_leaf_gemm_applies(mb, kb, nb)) {
+    return 0;
+  }
+  return tail_scratch_bytes(leaf_plan(rank, mb, kb, nb).split);
+}
+
+// ------------------------------------------------ allocation-free variant
+//
+// fastmm_leaf_products_noalloc keeps the split-K tail's fp32 parts in this
+// file-scope device array instead of caller memory. Its size is the most the
+// tail planner asks for on a 256-CU MI355X: at most 3/4 of the CUs' worth of
+// parts (192), each one 256 x 256 fp32 tile. Every process that loads the
+// library holds one copy per GPU it runs on until it exits. Host code never
+// passes the array's name to a kernel (on the host it is only a stand-in
+// symbol): it uses the device address hipGetSymbolAddress returns, looked up
+// once per device on that device's first call.
+constexpr int64_t kStaticScratchBytes = int64_t{192} * kTile * kTile * static_cast<int64_t>(sizeof(float));
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> scratch_address[kMaxDevices];  // zero-initialized
+std::mutex scratch_lookup;
+
+// The current device's address of `scratch` (looked up on first use).
+int static_scratch(void** address) {
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) {
+    (void)hipGetLastError();
+    return fail(FASTMM_ERROR_LAUNCH, "leaf products (no-alloc): no usable current device");
+  }
+  void* known = scratch_address[device].load(std::memory_order_acquire);
+  if (known == nullptr) {
+    std::lock_guard<std::mutex> guard(scratch_lookup);
+    known = scratch_address[device].load(std::memory_order_acquire);
+    if (known == nullptr) {
+      const hipError_t status = hipGetSymbolAddress(&known, HIP_SYMBOL(scratch));
+      if (status != hipSuccess || known == nullptr) {
+        (void)hipGetLastError();
+        return fail(FASTMM_ERROR_LAUNCH, "leaf products (no-alloc): scratch address on device %d: %s", device,
+                    hipGetErrorString(status));
+      }
+      scratch_address[device].store(known, std::memory_order_release);
+    }
+  }
+  *address = known;
+  return FASTMM_OK;
+}
+
+}  // namespace fastmm
+
+extern "C" int fastmm_leaf_products(int rank, int operand_dtype, const void* left_transformed,
+                                    const void* right_transformed, void* products,
+                                    int products_dtype, int64_t block_rows, int64_t block_inner,
+                                    int64_t block_columns, void* scratch, int64_t scratch_bytes,
+                                    void* stream) {
+  clear_error();
+  if (scratch_bytes < 0 || (scratch == nullptr && scratch_bytes != 0)) {
+    return fail(FASTMM_ERROR_ARGUMENT, "leaf products: scratch of %lld bytes at null",
+                static_cast<long long>(scratch_bytes));
+  }
+  if (int status = check_leaf_arguments(rank, operand_dtype, left_transformed, right_transformed, products,
+                                        products_dtype, block_rows, block_inner, block_columns)) {
+    return status;
+  }
+  return run_leaf_products(rank, operand_dtype, left_transformed, right_transformed, products, products_dtype,
+                           block_rows, block_inner, block_columns, scratch, scratch_bytes,
+                           static_cast<hipStream_t>(stream));
+}
+
+extern "C" int fastmm_leaf_products_noalloc(int rank, int operand_dtype, const void* left_transformed,
+                                            const void* right_transformed, void* products, int products_dtype,
+                                            int64_t block_rows, int64_t block_inner, int64_t block_columns,
+                                            void* stream) {
+  clear_error();
+  if (int status = check_leaf_arguments(rank, operand_dtype, left_transformed, right_transformed, products,
+                                        products_dtype, block_rows, block_inner, block_columns)) {
+    return status;
+  }
+  const int64_t needed = planned_scratch_bytes(rank, products_dtype, block_rows, block_inner, block_columns);
+  if (needed > kStaticScratchBytes) {
+    return fail(FASTMM_ERROR_UNSUPPORTED,
+                "leaf products (no-alloc): the split-K tail needs %lld bytes of scratch, above the library's "
+                "static %lld; use fastmm_leaf_products with caller scratch",
+                static_cast<long long>(needed), static_cast<long long>(kStaticScratchBytes));
+  }
+  void* address = nullptr;
+  if (needed > 0) {
+    if (int status = static_scratch(&address)) return status;
+  }
+  return run_leaf_products(rank, operand_dtype, left_transformed, right_transformed, products, products_dtype,
+                           block_rows, block_inner, block_columns, address, needed,
+                           static_cast<hipStream_t>(stream));
 }
 
 extern "C" int fastmm_leaf_scratch_bytes(int rank, int operand_dtype, int products_dtype, int64_t block_rows,
@@ -1498,11 +1591,6 @@ extern "C" int fastmm_leaf_scratch_bytes(int rank, int operand_dtype, int produc
                 products_dtype);
   }
   // the split-K tail runs on the 16x16x32 path (16-byte aligned buffers assumed)
-  const int64_t out_align = products_dtype == kFP32 ? 4 : 8;
-  if (block_inner % fast::BK != 0 || block_inner < 3 * fast::BK || block_columns % out_align != 0 ||
-      !mfma16_leaf_gemm_applies(block_rows, block_inner, block_columns)) {
-    return FASTMM_OK;
-  }
-  *bytes = tail_scratch_bytes(leaf_plan(rank, block_rows, block_inner, block_columns).split);
+  *bytes = planned_scratch_bytes(rank, products_dtype, block_rows, block_inner, block_columns);
   return FASTMM_OK;
 }

@@ -30,6 +30,7 @@ SIGNATURES: dict[str, list] = {
     "fastmm_weight_transform": [_INT, _INT, _INT, _PTR, _PTR, _I64, _I64, _PTR],
     "fastmm_right_transform": [_INT, _INT, _INT, _PTR, _PTR, _I64, _I64, _PTR],
     "fastmm_leaf_products": [_INT, _INT, _PTR, _PTR, _PTR, _INT, _I64, _I64, _I64, _PTR, _I64, _PTR],
+    "fastmm_leaf_products_noalloc": [_INT, _INT, _PTR, _PTR, _PTR, _INT, _I64, _I64, _I64, _PTR],
     "fastmm_leaf_scratch_bytes": [_INT, _INT, _INT, _I64, _I64, _I64, ctypes.POINTER(_I64)],
     "fastmm_reconstruct": [_INT, _INT, _PTR, _PTR, _INT, _PTR, _I64, _I64, _PTR],
     "fastmm_scheme_info": [_INT, ctypes.POINTER(_INT), ctypes.POINTER(_INT)],

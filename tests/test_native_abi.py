@@ -26,6 +26,7 @@ def test_header_declares_the_stage_entry_points() -> None:
         "fastmm_right_transform",
         "fastmm_leaf_products",
         "fastmm_leaf_scratch_bytes",
+        "fastmm_leaf_products_noalloc",
         "fastmm_reconstruct",
         "fastmm_abi_version",
         "fastmm_last_error",
@@ -71,6 +72,11 @@ def test_compiled_scheme_digests_match_verified_certificates() -> None:
         (lambda lib: lib.fastmm_leaf_products(7, 1, 16, 16, 16, 1, 2, 2, 2, None, 64, None), b"scratch of 64 bytes"),
         (lambda lib: lib.fastmm_leaf_products(7, 1, 16, 16, 16, 1, 2, 2, 2, 16, -1, None), b"scratch of -1 bytes"),
         (lambda lib: lib.fastmm_leaf_scratch_bytes(7, 1, 1, 2, 2, 2, None), b"null result pointer"),
+        (lambda lib: lib.fastmm_leaf_products_noalloc(7, 1, None, 16, 16, 1, 2, 2, 2, None), b"null pointer"),
+        (lambda lib: lib.fastmm_leaf_products_noalloc(7, 2, 16, 16, 16, 2, 2, 2, 2, None), b"operands must be"),
+        (lambda lib: lib.fastmm_leaf_products_noalloc(7, 1, 16, 16, 16, 0, 2, 2, 2, None), b"products must be fp32 or"),
+        (lambda lib: lib.fastmm_leaf_products_noalloc(0, 1, 16, 16, 16, 1, 2, 2, 2, None), b"positive"),
+        (lambda lib: lib.fastmm_leaf_products_noalloc(7, 1, 16, 16, 16, 1, 1 << 20, 1 << 12, 2, None), b"2^31"),
         (lambda lib: lib.fastmm_leaf_scratch_bytes(7, 2, 2, 2, 2, 2, ctypes.byref(ctypes.c_int64())),
          b"unsupported element types"),
         (lambda lib: lib.fastmm_leaf_scratch_bytes(7, 1, 1, 0, 2, 2, ctypes.byref(ctypes.c_int64())), b"positive"),
