@@ -140,11 +140,14 @@ int fastmm_leaf_scratch_bytes(int rank, int operand_dtype, int products_dtype, i
  * output[rows, columns] in dtype, with an optional bias[columns] (NULL = none)
  * added in fp32 after the scheme's sum. Replaces _reconstruct / _reconstruct_bias + output_transform[_bias]_kernel
  * (runtime.py:657-698; rank7_2x2x2.py:207-345).
- * The 8x8-block scheme with fp16 products, no bias and columns % 64 == 0 runs
- * the reference's dense form instead (Rank343Plan._reconstruct,
- * runtime.py:938-962: every output block as one fp32-accumulated MFMA
- * contraction of the products with the scheme's -1/0/1 output matrix); its
- * other inputs run the output circuit. */
+ * The 8x8-block scheme runs the reference's dense form instead
+ * (Rank343Plan._reconstruct, runtime.py:938-962: every output block as one
+ * fp32-accumulated MFMA contraction of the products with the scheme's -1/0/1
+ * output matrix) when the products are fp16, there is no bias, columns % 64
+ * == 0 (whole 8-column blocks of whole 8-position groups), the products are
+ * 16-byte aligned and the output 8-byte aligned; its other inputs run the
+ * output circuit. The two forms agree up to fp32 summation order, so results
+ * can differ in the last bit between them. */
 int fastmm_reconstruct(int scheme, int products_dtype, const void* products, const void* bias,
                        int dtype, void* output, int64_t rows, int64_t columns, void* stream);
 

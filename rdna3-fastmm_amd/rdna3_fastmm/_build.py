@@ -10,7 +10,11 @@ The 16x16x32 leaf-GEMM kernels issue their MFMAs as inline asm, whose result
 latency the compiler cannot see. The build therefore also emits the device
 assembly of ``leaf_gemm.hip`` and refuses to produce the library if any
 compiler-generated instruction touches an accumulator register written by an
-asm MFMA before a fence (three ``s_nop 7``) has covered its latency.
+asm MFMA before a fence (three ``s_nop 7``) has covered its latency. The
+thin-row kernel issues its global loads as inline asm with hand-written
+``s_waitcnt vmcnt`` waits; the same check refuses a build in which any
+instruction reads or writes a load's destination registers while that load
+can still be in flight.
 """
 
 from __future__ import annotations
@@ -145,6 +149,64 @@ def fence_violations(assembly: str) -> list[str]:
     return violations
 
 
+ASM_LOAD_CHECKED_KERNELS = re.compile(r"^(_ZN6fastmm4thin\S*):", re.MULTILINE)
+_VGPR = re.compile(r"(?<![a-z_])v(?:\[(\d+):(\d+)\]|(\d+)\b)")
+_VMCNT = re.compile(r"vmcnt\((\d+)\)")
+_VMEM_PREFIXES = ("global_", "buffer_", "flat_", "scratch_")
+
+
+def _vgprs(operands: str) -> set[int]:
+    registers: set[int] = set()
+    for low, high, single in _VGPR.findall(operands):
+        if single:
+            registers.add(int(single))
+        else:
+            registers.update(range(int(low), int(high) + 1))
+    return registers
+
+
+def in_flight_load_violations(assembly: str, kernels: re.Pattern = ASM_LOAD_CHECKED_KERNELS) -> list[str]:
+    """Instructions that touch a vector load's destination while the load may be in flight.
+
+    Vector memory operations complete in issue order as far as ``vmcnt`` is
+    concerned, so each kernel is scanned in layout order with a queue of the
+    VMEM operations issued so far (stores hold a place in it without
+    registers); ``s_waitcnt vmcnt(n)`` retires all but the newest ``n``. Any
+    other instruction naming a VGPR of a queued load is a violation: it would
+    read the register before the data arrives or overwrite it before the load
+    lands. A load whose destination or address overlaps a queued load's
+    destination is one too.
+    """
+    violations: list[str] = []
+    for match in kernels.finditer(assembly):
+        name = match.group(1)
+        body = assembly[match.end():]
+        body = body[: body.find("s_endpgm")]
+        queue: list[set[int]] = []
+        for line in body.splitlines():
+            text = line.split(";", 1)[0].strip()
+            if not text or text.endswith(":") or text.startswith("."):
+                continue
+            opcode, _, operands = text.partition(" ")
+            if opcode == "s_waitcnt":
+                counted = _VMCNT.search(operands)
+                if counted:
+                    del queue[: max(0, len(queue) - int(counted.group(1)))]
+                continue
+            in_flight = set().union(*queue) if queue else set()
+            if opcode.startswith(_VMEM_PREFIXES):
+                fields = [field.strip() for field in operands.split(",")]
+                is_load = "_load" in opcode
+                touched = _vgprs(operands)
+                if touched & in_flight:
+                    violations.append(f"{name}: {text}")
+                queue.append(_vgprs(fields[0]) if is_load and fields else set())
+                continue
+            if _vgprs(operands) & in_flight:
+                violations.append(f"{name}: {text}")
+    return violations
+
+
 def _check_device_assembly() -> None:
     target = BUILD_DIR / (Path(ASM_CHECKED_SOURCE).stem + ".s")
     command = [_hipcc(), *COMMON_FLAGS, "--cuda-device-only", "-S", str(SOURCE_DIR / ASM_CHECKED_SOURCE), "-o", str(target)]
@@ -158,6 +220,12 @@ def _check_device_assembly() -> None:
     if violations:
         listing = "\n".join(violations[:20])
         raise RuntimeError(f"{ASM_CHECKED_SOURCE}: accumulator accessed inside MFMA latency:\n{listing}")
+    if not ASM_LOAD_CHECKED_KERNELS.search(assembly):
+        raise RuntimeError(f"{ASM_CHECKED_SOURCE}: no thin-row kernels found to check")
+    violations = in_flight_load_violations(assembly)
+    if violations:
+        listing = "\n".join(violations[:20])
+        raise RuntimeError(f"{ASM_CHECKED_SOURCE}: load destination accessed while in flight:\n{listing}")
 
 
 def build_library(verbose: bool = False) -> Path:

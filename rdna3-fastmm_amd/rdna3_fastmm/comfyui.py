@@ -1,99 +1,101 @@
-"""ComfyUI node: compile a diffusion model with the ``rdna3-fastmm`` backend.
+"""ComfyUI custom node that compiles a diffusion model with the ``rdna3-fastmm`` backend.
 
-reference ``src/rdna3_fastmm/comfyui.py:76-119`` (and the custom-node entry
-``__init__.py:1-26``, here the repository root's ``__init__.py``). The node
-keeps the reference's class key ``RDNA3FastMMCompile``, so saved workflows
-load unchanged. It clones the MODEL (dynamic shapes off) and asks ComfyUI's
-``comfy_api.torch_helpers.set_torch_compile_wrapper`` (ComfyUI >= 0.19.0) to
-wrap only ``diffusion_model`` with ``torch.compile`` on this package's Dynamo
-backend. Guards on ComfyUI's per-call ``transformer_options`` are dropped,
-as in the reference, so changing them does not recompile. The backend then
-rewrites only the BF16 Linears in the MI355X dispatch table; everything else
-compiles with standard Inductor.
+Counterpart of the reference's node (``src/rdna3_fastmm/comfyui.py:76-119``;
+custom-node entry ``__init__.py:1-26``, here the repository root's
+``__init__.py``). Saved workflows reference a node by its class key, so the
+key ``RDNA3FastMMCompile``, its single MODEL input and output, and the two
+refusal messages stay as the reference has them; the rest is this package's.
 
-The node refuses to run (``RuntimeError``, before cloning) when the runtime is
-not the tested MI355X stack. There is no Python-version gate: this package
-runs on Python 3.10+, unlike the reference's 3.12/3.13 requirement.
+What the node does to a MODEL: it resolves its toolchain first (the MI355X
+runtime gate, ComfyUI's ``comfy_api.torch_helpers.set_torch_compile_wrapper``
+from ComfyUI 0.19.0 on, and this package's Dynamo backend) and refuses with a
+``RuntimeError`` before touching the model if any part is missing. It then
+patches a clone of the model (dynamic shapes off) so that only the
+``diffusion_model`` submodule is compiled with the backend, which rewrites
+just the BF16 Linears in the MI355X dispatch table and leaves the rest to
+standard Inductor. ComfyUI hands every call a new ``transformer_options``
+dict; guards on it are dropped so that does not force recompiles.
 """
 
 from __future__ import annotations
 
-from importlib import import_module
+import importlib
 import logging
-from typing import Any, Callable, Protocol, Sequence
+from typing import Any, Callable, NamedTuple, Sequence
 
-BackendCompiler = Callable[..., object]
-logger = logging.getLogger(__name__)
-
-
-class ComfyModel(Protocol):
-    def clone(self, disable_dynamic: bool = False) -> "ComfyModel": ...
+NODE_KEY = "RDNA3FastMMCompile"
+COMPILED_SUBMODULES = ("diffusion_model",)
+MINIMUM_COMFYUI = "0.19.0"
+_LOG = logging.getLogger(__name__)
 
 
-class GuardEntry(Protocol):
-    name: str
+def skip_comfy_transformer_option_guards(guards: Sequence[Any]) -> list[bool]:
+    """Dynamo guard filter (True keeps a guard): every guard except those on the
+    per-call ``transformer_options`` dict ComfyUI passes to the model."""
+    return ["transformer_options" not in str(getattr(guard, "name", "")) for guard in guards]
 
 
-def skip_comfy_transformer_option_guards(guard_entries: Sequence[GuardEntry]) -> list[bool]:
-    """Keep every Dynamo guard except those on ComfyUI's ``transformer_options``."""
-    return ["transformer_options" not in entry.name for entry in guard_entries]
+class Toolchain(NamedTuple):
+    """What compiling needs from the environment."""
+
+    wrap_model: Callable[..., None]  # ComfyUI's set_torch_compile_wrapper
+    backend: Callable[..., object]  # rdna3_fastmm.inductor.compile_backend
 
 
-def _unsupported_reason() -> str | None:
+def _runtime_problem() -> str | None:
+    """Why this machine is not the tested MI355X stack (None when it is)."""
     try:
-        runtime = import_module("rdna3_fastmm.runtime")
-    except ModuleNotFoundError as error:
+        from .runtime import unsupported_runtime_reason
+    except ModuleNotFoundError as error:  # e.g. torch absent from ComfyUI's environment
         return f"missing Python dependency {error.name}"
-    return runtime.unsupported_runtime_reason()
+    return unsupported_runtime_reason()
 
 
-def _load_compile_backend() -> BackendCompiler:
-    return import_module("rdna3_fastmm.inductor").compile_backend
-
-
-def _load_compile_setter() -> Callable[..., None]:
+def toolchain() -> Toolchain:
+    """Resolve the node's dependencies, or raise RuntimeError naming the missing one."""
+    problem = _runtime_problem()
+    if problem is not None:
+        raise RuntimeError(f"Cannot enable RDNA3 FastMM: {problem}")
     try:
-        helpers = import_module("comfy_api.torch_helpers")
+        helpers = importlib.import_module("comfy_api.torch_helpers")
     except ModuleNotFoundError as error:
-        if error.name is not None and error.name.startswith("comfy_api"):
-            raise RuntimeError("RDNA3 FastMM requires ComfyUI 0.19.0 or newer") from error
+        if (error.name or "").startswith("comfy_api"):
+            raise RuntimeError(f"RDNA3 FastMM requires ComfyUI {MINIMUM_COMFYUI} or newer") from error
         raise
-    return helpers.set_torch_compile_wrapper
+    backend = importlib.import_module(f"{__package__}.inductor").compile_backend
+    return Toolchain(wrap_model=helpers.set_torch_compile_wrapper, backend=backend)
 
 
 class RDNA3FastMMCompile:
-    @classmethod
-    def INPUT_TYPES(cls) -> dict[str, dict[str, tuple[str]]]:
-        return {"required": {"model": ("MODEL",)}}
+    """MODEL -> MODEL whose diffusion model runs through the FastMM Linear rewrite."""
 
     RETURN_TYPES = ("MODEL",)
     RETURN_NAMES = ("model",)
     FUNCTION = "compile_model"
     CATEGORY = "model_patches/compile"
-    DESCRIPTION = (
-        "Compiles the diffusion model with FastMM on MI355X. BF16 Linear shapes with a "
-        "measured win use reduced-multiplication HIP kernels; all other operations remain "
-        "ordinary PyTorch Inductor operations."
-    )
     EXPERIMENTAL = True
+    DESCRIPTION = (
+        "Compiles the diffusion model with FastMM on MI355X: BF16 Linear shapes with a measured "
+        "win run reduced-multiplication HIP kernels, everything else stays ordinary Inductor code."
+    )
 
-    def compile_model(self, model: ComfyModel) -> tuple[Any]:
-        reason = _unsupported_reason()
-        if reason is not None:
-            raise RuntimeError(f"Cannot enable RDNA3 FastMM: {reason}")
-        set_compile_wrapper = _load_compile_setter()
-        backend = _load_compile_backend()
-        compiled = model.clone(disable_dynamic=True)
-        set_compile_wrapper(
-            model=compiled,
-            backend=backend,
+    @classmethod
+    def INPUT_TYPES(cls) -> dict[str, dict[str, tuple[str]]]:
+        return {"required": {"model": ("MODEL",)}}
+
+    def compile_model(self, model: Any) -> tuple[Any]:
+        tools = toolchain()  # refuse before cloning anything
+        patched = model.clone(disable_dynamic=True)
+        tools.wrap_model(
+            model=patched,
+            backend=tools.backend,
             options={"guard_filter_fn": skip_comfy_transformer_option_guards},
             dynamic=False,
-            keys=["diffusion_model"],
+            keys=list(COMPILED_SUBMODULES),
         )
-        logger.info("Enabled RDNA3 FastMM for the ComfyUI diffusion model")
-        return (compiled,)
+        _LOG.info("rdna3-fastmm: %s compiled with the FastMM backend", ", ".join(COMPILED_SUBMODULES))
+        return (patched,)
 
 
-NODE_CLASS_MAPPINGS = {"RDNA3FastMMCompile": RDNA3FastMMCompile}
-NODE_DISPLAY_NAME_MAPPINGS = {"RDNA3FastMMCompile": "RDNA3 FastMM Compile"}
+NODE_CLASS_MAPPINGS = {NODE_KEY: RDNA3FastMMCompile}
+NODE_DISPLAY_NAME_MAPPINGS = {NODE_KEY: "RDNA3 FastMM Compile"}

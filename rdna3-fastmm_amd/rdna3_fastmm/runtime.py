@@ -756,10 +756,13 @@ class Rank343Plan(_Plan):
     """<8,8,8> rank 343 (1661 additions), FP16 ``mm`` only; reference runtime.py:883-962.
 
     Only the ``mm`` path (``pack_right``, ``run``, ``run_packed``): the reference
-    offers no Linear plan for it. The recombination evaluates the certificate's
-    output circuit in fp32, like the other schemes; the reference evaluates the
-    same integer combination as one dense FP16 dot with fp32 accumulation
-    (``MFMA_OUTPUT_COEFFICIENTS``), so the two agree up to fp32 summation order.
+    offers no Linear plan for it. The recombination is the reference's dense
+    form (``MFMA_OUTPUT_COEFFICIENTS``: each output block one FP16 MFMA
+    contraction of the products with the -1/0/1 output matrix, fp32
+    accumulation) when the plan's buffers allow it: fp16 products, columns a
+    multiple of 64, products 16-byte and output 8-byte aligned (always so for
+    the plan's own workspace and a fresh output). Otherwise the certificate's
+    output circuit runs in fp32; the two agree up to fp32 summation order.
     ``prepacked_shapes`` and ``dynamic_shapes`` hold MI355X-measured wins only.
     """
 
@@ -768,9 +771,10 @@ class Rank343Plan(_Plan):
     rank = 343
     scheme_size = 8
     precision_pairs = frozenset({(torch.float16, torch.float16)})
-    # Prepacked 16384^3 beat FP16 torch.mm on two MI355X boxes (1.04x, 1.07x;
-    # bench.py --config c6-rank343); the dynamic path (right transform per call)
-    # does not (0.89x). Smaller squares lose (0.74x at 8192^3).
+    # Prepacked 16384^3 beat FP16 torch.mm on two MI355X boxes (1.09-1.12x with
+    # the dense recombination; bench.py --config c6-rank343); the dynamic path
+    # (right transform per call) does not (0.89x with the circuit recombination).
+    # Smaller squares lose (0.74x at 8192^3).
     prepacked_shapes = frozenset({(16_384, 16_384, 16_384)})
 
 

@@ -47,9 +47,7 @@ def test_node_clones_and_wraps_only_the_diffusion_model(monkeypatch) -> None:
     def set_wrapper(**kwargs):
         captured.update(kwargs)
 
-    monkeypatch.setattr(comfyui, "_unsupported_reason", lambda: None)
-    monkeypatch.setattr(comfyui, "_load_compile_backend", lambda: backend)
-    monkeypatch.setattr(comfyui, "_load_compile_setter", lambda: set_wrapper)
+    monkeypatch.setattr(comfyui, "toolchain", lambda: comfyui.Toolchain(set_wrapper, backend))
     source = FakeModel()
     (compiled,) = comfyui.RDNA3FastMMCompile().compile_model(source)
     assert compiled is captured["model"] and compiled is not source
@@ -61,35 +59,38 @@ def test_node_clones_and_wraps_only_the_diffusion_model(monkeypatch) -> None:
 
 def test_node_rejects_an_unsupported_runtime_before_cloning(monkeypatch) -> None:
     source = FakeModel()
-    monkeypatch.setattr(comfyui, "_unsupported_reason", lambda: "unsupported test runtime")
+    monkeypatch.setattr(comfyui, "_runtime_problem", lambda: "unsupported test runtime")
     with pytest.raises(RuntimeError, match="Cannot enable RDNA3 FastMM: unsupported test runtime"):
         comfyui.RDNA3FastMMCompile().compile_model(source)
     assert source.clone_arguments == []
 
 
-def test_unsupported_reason_is_the_runtime_gate() -> None:
+def test_runtime_problem_is_the_runtime_gate() -> None:
     # the runtime gate's reason (None on the tested MI355X stack) comes through unchanged
     from rdna3_fastmm.runtime import unsupported_runtime_reason
 
-    assert comfyui._unsupported_reason() == unsupported_runtime_reason()
+    assert comfyui._runtime_problem() == unsupported_runtime_reason()
 
 
-def test_compile_setter_requires_current_comfyui(monkeypatch) -> None:
+def test_toolchain_requires_current_comfyui(monkeypatch) -> None:
     def missing(name: str) -> ModuleType:
         raise ModuleNotFoundError(f"No module named {name!r}", name=name)
 
-    monkeypatch.setattr(comfyui, "import_module", missing)
+    monkeypatch.setattr(comfyui, "_runtime_problem", lambda: None)
+    monkeypatch.setattr(comfyui.importlib, "import_module", missing)
     with pytest.raises(RuntimeError, match="requires ComfyUI 0.19.0 or newer"):
-        comfyui._load_compile_setter()
+        comfyui.toolchain()
 
 
-def test_compile_setter_is_comfyuis_helper(monkeypatch) -> None:
+def test_toolchain_uses_comfyuis_helper_and_the_backend(monkeypatch) -> None:
     helpers = ModuleType("comfy_api.torch_helpers")
     helpers.set_torch_compile_wrapper = lambda **kwargs: None
     monkeypatch.setitem(sys.modules, "comfy_api", ModuleType("comfy_api"))
     monkeypatch.setitem(sys.modules, "comfy_api.torch_helpers", helpers)
-    assert comfyui._load_compile_setter() is helpers.set_torch_compile_wrapper
-    assert comfyui._load_compile_backend().__name__ == "compile_backend"
+    monkeypatch.setattr(comfyui, "_runtime_problem", lambda: None)
+    tools = comfyui.toolchain()
+    assert tools.wrap_model is helpers.set_torch_compile_wrapper
+    assert tools.backend.__name__ == "compile_backend"
 
 
 def test_node_contract_is_exported() -> None:

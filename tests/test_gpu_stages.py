@@ -167,13 +167,14 @@ def test_reconstruct_bit_exact(key, shape, product_dtype) -> None:
             assert np.array_equal(_bits(out), expected.view(np.int16)), (dtype, use_bias)
 
 
-@pytest.mark.parametrize("shape", ((64, 64), (37, 128), (300, 192), (1000, 512), (2050, 1024)))
+@pytest.mark.parametrize("shape", ((64, 64), (37, 128), (300, 192), (1000, 576), (2050, 1024)))
 def test_rank343_dense_recombination_matches_the_dense_oracle(shape) -> None:
     """Rank 343, fp16 products and output, no bias: the dense MFMA contraction
     (reference output_transform_mfma_kernel) against the oracle's dense form.
     The shapes cover one and many tiles of 64 positions per wave, a partial last
-    tile (plane 2000 = 31.25 tiles at 1000 x 512), padded output rows
-    (M % 8 != 0) and small integers, which must come out exact."""
+    tile (plane 5 x 16 = 1.25 tiles at 37 x 128; 125 x 72 = 140.6 tiles at
+    1000 x 576), padded output rows (M % 8 != 0) and small integers, which must
+    come out exact."""
     m, n = shape
     print(f"\n[case] rank343 dense recombination {shape}", flush=True)
     scheme = load_scheme("rank343")

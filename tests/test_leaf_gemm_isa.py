@@ -101,3 +101,40 @@ def test_main_loop_shape(assembly) -> None:
         assert count("s_barrier") == 4, name
         for forbidden in ("v_accvgpr", "scratch_", "v_mov", "global_load", "flat_"):
             assert count(forbidden) == 0, (name, forbidden)
+
+
+def test_thin_row_kernels_touch_no_load_in_flight(assembly) -> None:
+    names = [m.group(1) for m in _build.ASM_LOAD_CHECKED_KERNELS.finditer(assembly)]
+    for variant in ("ILi1ELi1E", "ILi1ELi2E", "ILi0ELi0E", "ILi0ELi2E"):
+        assert any(variant in n for n in names), (variant, names)
+    assert _build.in_flight_load_violations(assembly) == []
+
+
+def test_load_checker_catches_a_planted_read(assembly) -> None:
+    # copy a register of the first asm load's destination right after the load
+    match = re.search(r"(\tglobal_load_dwordx4 v\[(\d+):\d+\], v\[\d+:\d+\], off\n)",
+                      assembly[_build.ASM_LOAD_CHECKED_KERNELS.search(assembly).end():])
+    assert match
+    planted = assembly.replace(match.group(1), match.group(1) + f"\tv_mov_b32_e32 v250, v{match.group(2)}\n", 1)
+    found = _build.in_flight_load_violations(planted)
+    assert len(found) == 1 and f"v_mov_b32_e32 v250, v{match.group(2)}" in found[0]
+
+
+def test_load_checker_on_synthetic_listing() -> None:
+    head = "_ZN6fastmm4thinkE:\n"
+    loads = "\tglobal_load_dwordx4 v[4:7], v[0:1], off\n\tglobal_load_dwordx4 v[8:11], v[2:3], off\n"
+    use = "\tv_add_u32_e32 v20, v5, v9\n"
+    end = "\ts_endpgm\n"
+    assert len(_build.in_flight_load_violations(head + loads + use + end)) == 1
+    # vmcnt(1) retires the older load only: v5 is ready, v9 is not
+    assert len(_build.in_flight_load_violations(head + loads + "\ts_waitcnt vmcnt(1)\n" + use + end)) == 1
+    assert _build.in_flight_load_violations(head + loads + "\ts_waitcnt vmcnt(1)\n\tv_mov_b32_e32 v20, v5\n" + end) == []
+    assert _build.in_flight_load_violations(head + loads + "\ts_waitcnt vmcnt(0)\n" + use + end) == []
+    # overwriting an address after issue is fine; overwriting a pending destination is not
+    assert _build.in_flight_load_violations(head + loads + "\tv_mov_b32_e32 v0, 0\n" + end) == []
+    assert len(_build.in_flight_load_violations(head + loads + "\tv_mov_b32_e32 v7, 0\n" + end)) == 1
+    # a store holds a place in the count: after a load and a store, vmcnt(1) retires the load, vmcnt(2) does not
+    store = "\tglobal_store_dwordx4 v[0:1], v[12:15], off\n"
+    one = "\tglobal_load_dwordx4 v[4:7], v[0:1], off\n"
+    assert _build.in_flight_load_violations(head + one + store + "\ts_waitcnt vmcnt(1)\n\tv_mov_b32_e32 v20, v5\n" + end) == []
+    assert len(_build.in_flight_load_violations(head + one + store + "\ts_waitcnt vmcnt(2)\n\tv_mov_b32_e32 v20, v5\n" + end)) == 1
