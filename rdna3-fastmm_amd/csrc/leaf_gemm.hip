@@ -894,62 +894,67 @@ void persistent_kernel(const half_t* __restrict__ A, const half_t* __restrict__ 
     set_loads(t + 1 < count ? logical + stride : -1);
     boundary_group();
 
-    // Epilogue: four chunks of 64 rows through the staging area.
+    // Epilogue: each wave stages only its own 128 x 128 quadrant, in four
+    // passes of 32 rows through a private 8 KB slice of the staging area, so
+    // no wave waits for another. Lane (r = lane % 16, g = lane / 16) writes
+    // the 4 columns 16 j + 4 g .. +3 of quadrant row 16 ii + r (8 bytes) into
+    // 16-byte chunk (2 j + g / 2) ^ r of a 256-byte staging row (bytes 8 (g % 2)
+    // within it): for each j the 64 lanes fill all 64 banks twice over, with no
+    // conflict. It reads back 16-byte chunks (lane % 16) of rows 4 h + lane / 16
+    // and stores 4 quadrant rows x 256 bytes per instruction. The tile's base
+    // offset goes in the stores' scalar offset; lanes outside the leaf get an
+    // offset past the buffer and write nothing.
     int leaf, tm, tn;
     tile_of(logical, tiles_m, tiles_n, 8, leaf, tm, tn);
-    const unsigned m0 = tm * kTile, n0 = tn * kTile;
+    const unsigned m0 = tm * kTile + wm * 128, n0 = tn * kTile + wn * 128;  // quadrant origin
     const __amdgpu_buffer_rsrc_t p_rsrc = __builtin_amdgcn_make_buffer_rsrc(
         P + static_cast<int64_t>(leaf) * Mb * Nb, 0, Mb * Nb * 2, 0x00020000);
     // lane recomputed here (every lane is active), so no lane-derived value
     // stays live across the K loop
     int lane_now;
     asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane_now));
-    const int er = lane_now & 15, eg = lane_now >> 4;
-    const int tid_now = wave * 64 + lane_now;
+    const unsigned er = lane_now & 15, eg = lane_now >> 4;
+    const unsigned wave_stage = stage_base + static_cast<unsigned>(wave) * (32 * 256);
+    unsigned write_at[FN], read_at[4];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) write_at[j] = wave_stage + er * 256 + (((2 * j + (eg >> 1)) ^ er) << 4) + ((eg & 1) << 3);
+#pragma unroll
+    for (int h = 0; h < 4; ++h) read_at[h] = wave_stage + (4 * h + eg) * 256 + ((er ^ ((4 * h + eg) & 15)) << 4);
+    const unsigned nb_u = static_cast<unsigned>(Nb);
+    const unsigned lane_offset = (eg * nb_u + er * 8) * 2;  // row eg, column 8 er of a 4-row store
+    const unsigned mb_u = static_cast<unsigned>(Mb);
+    const bool column_inside = n0 + er * 8 < nb_u;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      // Chunk c: tile rows 32c .. 32c + 31 of each half (wm = 0, 1), that is
-      // accumulator rows i = 2c, 2c + 1 of every wave. Staging row
-      // wm*32 + ii*16 + er holds tile row wm*128 + (2c + ii)*16 + er; lane
-      // (er, eg) writes columns wn*128 + j*16 + 4*eg .. +3 (8 bytes).
 #pragma unroll
       for (int ii = 0; ii < 2; ++ii) {
         const int i = 2 * c + ii;
-        const unsigned row = wm * 32 + ii * 16 + er;
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
-          const unsigned chunk = wn * 16 + 2 * j + (eg >> 1);
-          const unsigned at = stage_base + row * (kTile * 2) + ((chunk ^ (row & 15)) << 4) + ((eg & 1) << 3);
           const uint2v v = {pack2<kOut>(acc[i][j][0], acc[i][j][1]), pack2<kOut>(acc[i][j][2], acc[i][j][3])};
-          asm volatile("ds_write_b64 %0, %1" : : "v"(at), "v"(v) : "memory");
+          asm volatile("ds_write_b64 %0, %1 offset:%2" : : "v"(write_at[j]), "v"(v), "i"(ii * 16 * 256) : "memory");
         }
       }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      fast::barrier();
-      // two halves of four 16-byte reads, then their stores
+      uint4v staged[8];
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        uint4v staged[4];
+      for (int h = 0; h < 8; ++h) {
+        asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(staged[h]) : "v"(read_at[h & 3]), "i"((h >> 2) * 16 * 256)
+                     : "memory");
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
-        for (int h = 0; h < 4; ++h) {
-          const unsigned row = (half * 4 + h) * 8 + (tid_now >> 5), chunk = tid_now & 31;
-          const unsigned at = stage_base + row * (kTile * 2) + ((chunk ^ (row & 15)) << 4);
-          asm volatile("ds_read_b128 %0, %1" : "=v"(staged[h]) : "v"(at) : "memory");
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-        for (int h = 0; h < 4; ++h) {
-          const unsigned sr = (half * 4 + h) * 8 + (tid_now >> 5);
-          const unsigned row = m0 + (sr >> 5) * 128 + 32 * c + (sr & 31);
-          const unsigned col = n0 + (tid_now & 31) * 8;
-          const bool inside = (row < static_cast<unsigned>(Mb)) & (col < static_cast<unsigned>(Nb));
-          const unsigned off = inside ? (row * static_cast<unsigned>(Nb) + col) * 2 : kOutOfRange;
-          __builtin_amdgcn_raw_buffer_store_b128(staged[h], p_rsrc, off, 0, 0);
-        }
-        asm volatile("" ::: "memory");
+      for (int h = 0; h < 8; ++h) {
+        const unsigned row0 = m0 + 32 * c + 4 * h;  // first of the instruction's 4 rows (uniform)
+        const bool inside = (row0 + eg < mb_u) && column_inside;
+        // a base past the leaf is zeroed so that the out-of-range offset cannot
+        // wrap into the buffer (in-range bases stay below Mb * Nb * 2 <= 2^31 - 1,
+        // which the launcher checks)
+        const unsigned base = (row0 < mb_u && n0 < nb_u) ? (row0 * nb_u + n0) * 2 : 0u;
+        __builtin_amdgcn_raw_buffer_store_b128(staged[h], p_rsrc, inside ? lane_offset : kOutOfRange,
+                                               static_cast<int>(base), 0);
       }
       asm volatile("" ::: "memory");
-      if (c < 3) fast::barrier();  // every wave has read the chunk before the next is written
     }
     read_first_slice();
   }
