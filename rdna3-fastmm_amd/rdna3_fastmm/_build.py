@@ -33,6 +33,8 @@ INCLUDE_DIR = PACKAGE_DIR.parent.parent / "include"
 BUILD_DIR = PACKAGE_DIR.parent / "_build"
 LIBRARY_NAME = "libfastmm_amd.so"
 LIBRARY_PATH = PACKAGE_DIR / LIBRARY_NAME
+TORCH_OPS_SOURCE = "torch_ops.cpp"
+TORCH_OPS_PATH = PACKAGE_DIR / "libfastmm_torch.so"
 ARCH = "gfx950"
 
 SOURCES = ("abi_common.cpp", "transforms.hip", "leaf_gemm.hip")
@@ -228,8 +230,44 @@ def _check_device_assembly() -> None:
         raise RuntimeError(f"{ASM_CHECKED_SOURCE}: load destination accessed while in flight:\n{listing}")
 
 
+def build_torch_operators(verbose: bool = False) -> Path:
+    """Compile the PyTorch-ROCm operator library over libfastmm_amd.so (host code only).
+
+    A plain ``g++`` build against the installed torch headers and libraries
+    (torch's include paths, its C++ ABI setting, c10/c10_hip/torch_hip), linked
+    to ``libfastmm_amd.so`` next to it through ``$ORIGIN``. Loaded with
+    ``torch.ops.load_library``.
+    """
+    import torch
+    from torch.utils.cpp_extension import include_paths, library_paths
+
+    rocm = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+    compiler = shutil.which("g++") or shutil.which("c++")
+    if compiler is None:
+        raise RuntimeError("no host C++ compiler found for the torch operator library")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    temporary = TORCH_OPS_PATH.with_suffix(".so.tmp")
+    command = [
+        compiler, "-O2", "-std=c++17", "-shared", "-fPIC", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+        "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+        *[f"-I{path}" for path in include_paths()], f"-I{rocm / 'include'}", f"-I{INCLUDE_DIR}",
+        str(SOURCE_DIR / TORCH_OPS_SOURCE),
+        *[f"-L{path}" for path in library_paths()], f"-L{rocm / 'lib'}", f"-L{PACKAGE_DIR}",
+        "-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch_hip", "-ltorch", "-lamdhip64", "-lfastmm_amd",
+        "-Wl,-rpath,$ORIGIN", *[f"-Wl,-rpath,{path}" for path in library_paths()], "-o", str(temporary),
+    ]
+    result = subprocess.run(command, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"building {TORCH_OPS_PATH.name} failed:\n{result.stderr}")
+    os.replace(temporary, TORCH_OPS_PATH)
+    if verbose:
+        print(f"built {TORCH_OPS_PATH}")
+    return TORCH_OPS_PATH
+
+
 def build_library(verbose: bool = False) -> Path:
-    """Compile every source, check the leaf-GEMM assembly, link; returns the path."""
+    """Compile every source, check the leaf-GEMM assembly, link, then build the torch
+    operator library on top; returns the path of libfastmm_amd.so."""
     BUILD_DIR.mkdir(exist_ok=True)
     workers = min(len(SOURCES) + 1, max(1, (os.cpu_count() or 2) // 2))
     with ThreadPoolExecutor(max_workers=workers) as pool:
@@ -244,6 +282,7 @@ def build_library(verbose: bool = False) -> Path:
     os.replace(temporary, LIBRARY_PATH)
     if verbose:
         print(f"built {LIBRARY_PATH}")
+    build_torch_operators(verbose)
     return LIBRARY_PATH
 
 

@@ -3,11 +3,14 @@
 ``torch.ops.rdna3_fastmm.linear`` (rank 49) and
 ``torch.ops.rdna3_fastmm.linear_rank7`` keep the reference's schemas
 (``src/rdna3_fastmm/linear.py:50-167``): functional, ``(Tensor input, Tensor
-weight, Tensor? bias=None) -> Tensor``, any number of leading dimensions,
-with a fake (meta) implementation so Dynamo/Inductor treat them as opaque
-extern kernels. The reference builds them as ``triton_op``s so Inductor can
-see the Triton kernels; these are ``torch.library.custom_op``s over the HIP
-library, which Inductor calls as a fallback kernel.
+weight, Tensor? bias=None) -> Tensor``, any number of leading dimensions.
+The reference builds them as ``triton_op``s so Inductor sees the Triton
+kernels; here they are C++ operators of the PyTorch-ROCm extension
+``libfastmm_torch.so`` (``csrc/torch_ops.cpp``), which runs the whole call
+(planes, products, early release of the planes, output, recombination) as
+launches of the HIP library, with a fake (meta) implementation registered here
+so Dynamo/Inductor treat them as opaque extern kernels.
+``torch.ops.rdna3_fastmm.linear_rank48`` is the rank-48 counterpart.
 
 ``rewrite_eligible_linears`` replaces eligible ``aten.linear`` nodes of a
 graph before AOT compilation, exactly where the reference does
@@ -25,9 +28,8 @@ import torch
 from torch.fx import GraphModule, Node
 from torch.fx.passes.fake_tensor_prop import FakeTensorProp
 
-from . import _stages
-from .runtime import Rank7Plan, Rank48Plan, Rank49Plan, _check_library_scheme, _LinearPlan, operand_shape
-from .schemes import load_scheme
+from . import _torch_ops
+from .runtime import Rank7Plan, Rank48Plan, Rank49Plan, _LinearPlan
 
 LINEAR_TARGETS = frozenset({torch._C._nn.linear, torch.ops.aten.linear.default})
 MAX_LINEAR_ALLOCATION_FREE_FRACTION = 0.5
@@ -38,6 +40,7 @@ def _ceil_div(a: int, b: int) -> int:
 
 
 def _check_operands(name: str, input_tensor: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor]) -> None:
+    """The operators' argument checks (the C++ operators raise the same ValueErrors)."""
     if input_tensor.dtype not in (torch.bfloat16, torch.float16) or weight.dtype != input_tensor.dtype:
         raise ValueError(f"{name} needs bf16 or fp16 input and weight of one dtype")
     if input_tensor.device.type != "cuda" or weight.device != input_tensor.device:
@@ -55,65 +58,35 @@ def _check_operands(name: str, input_tensor: torch.Tensor, weight: torch.Tensor,
         raise ValueError(f"{name}: bias must be a contiguous [N] tensor of the input dtype")
 
 
-def _linear(plan_type: type, name: str, input_tensor: torch.Tensor, weight: torch.Tensor,
-            bias: Optional[torch.Tensor]) -> torch.Tensor:
-    """One dynamic linear through the scheme; temporaries freed before the output exists.
-
-    Stage order and the early release of A'/B' follow reference linear.py:66-153.
-    """
-    _check_operands(name, input_tensor, weight, bias)
-    scheme = load_scheme(plan_type.scheme_key)
-    _check_library_scheme(scheme)
-    inner = input_tensor.shape[-1]
-    columns = weight.shape[0]
-    flat = input_tensor.reshape(-1, inner)
-    rows = flat.shape[0]
-    s, rank = scheme.size, scheme.rank
-    mb, kb, nb = _ceil_div(rows, s), _ceil_div(inner, s), _ceil_div(columns, s)
-    device = input_tensor.device
-    left = torch.empty(operand_shape(rank, mb, kb), device=device, dtype=torch.float16)
-    right = torch.empty(operand_shape(rank, nb, kb), device=device, dtype=torch.float16)
-    _stages.left_transform(scheme, flat, left, rows, inner)
-    _stages.weight_transform(scheme, weight, right, columns, inner)
-    products = torch.empty((rank, mb, nb), device=device, dtype=torch.float16)
-    scratch_bytes = _stages.leaf_scratch_bytes(rank, torch.float16, torch.float16, mb, kb, nb, device)
-    scratch = torch.empty(scratch_bytes, device=device, dtype=torch.uint8) if scratch_bytes else None
-    _stages.leaf_products(rank, left, right, products, mb, kb, nb, scratch)
-    del left, right, scratch
-    output = torch.empty((rows, columns), device=device, dtype=input_tensor.dtype)
-    _stages.reconstruct(scheme, products, bias, output, rows, columns)
-    return output.reshape(*input_tensor.shape[:-1], columns)
-
-
-@torch.library.custom_op("rdna3_fastmm::linear", mutates_args=())
-def rdna3_linear(input_tensor: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
-    return _linear(Rank49Plan, "rdna3_fastmm::linear", input_tensor, weight, bias)
-
-
-@torch.library.custom_op("rdna3_fastmm::linear_rank7", mutates_args=())
-def rdna3_rank7_linear(
-    input_tensor: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None
-) -> torch.Tensor:
-    return _linear(Rank7Plan, "rdna3_fastmm::linear_rank7", input_tensor, weight, bias)
-
-
-@torch.library.custom_op("rdna3_fastmm::linear_rank48", mutates_args=())
-def rdna3_rank48_linear(
-    input_tensor: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None
-) -> torch.Tensor:
-    return _linear(Rank48Plan, "rdna3_fastmm::linear_rank48", input_tensor, weight, bias)
-
-
 def _fake_linear(input_tensor: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
     return input_tensor.new_empty((*input_tensor.shape[:-1], weight.shape[0]))
 
 
-for _op in (rdna3_linear, rdna3_rank7_linear, rdna3_rank48_linear):
-    _op.register_fake(_fake_linear)
+for _name in ("rdna3_fastmm::linear", "rdna3_fastmm::linear_rank7", "rdna3_fastmm::linear_rank48"):
+    torch.library.register_fake(_name)(_fake_linear)
 
-RDNA3_LINEAR_OP = torch.ops.rdna3_fastmm.linear.default
-RDNA3_RANK7_LINEAR_OP = torch.ops.rdna3_fastmm.linear_rank7.default
-RDNA3_RANK48_LINEAR_OP = torch.ops.rdna3_fastmm.linear_rank48.default
+RDNA3_LINEAR_OP = _torch_ops.linear
+RDNA3_RANK7_LINEAR_OP = _torch_ops.linear_rank7
+RDNA3_RANK48_LINEAR_OP = _torch_ops.linear_rank48
+
+
+def rdna3_linear(input_tensor: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``torch.ops.rdna3_fastmm.linear``: F.linear through the rank-49 scheme."""
+    return RDNA3_LINEAR_OP(input_tensor, weight, bias)
+
+
+def rdna3_rank7_linear(
+    input_tensor: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None
+) -> torch.Tensor:
+    """``torch.ops.rdna3_fastmm.linear_rank7``: F.linear through the rank-7 scheme."""
+    return RDNA3_RANK7_LINEAR_OP(input_tensor, weight, bias)
+
+
+def rdna3_rank48_linear(
+    input_tensor: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None
+) -> torch.Tensor:
+    """``torch.ops.rdna3_fastmm.linear_rank48``: F.linear through the rank-48 scheme."""
+    return RDNA3_RANK48_LINEAR_OP(input_tensor, weight, bias)
 
 
 def _node_tensor(node: Node) -> Optional[torch.Tensor]:

@@ -104,3 +104,44 @@ def test_leaf_scratch_query_without_a_device_reports_no_tail() -> None:
 def test_missing_library_fails_loudly(tmp_path: Path) -> None:
     with pytest.raises(_native.NativeLibraryError, match="not built"):
         _native.library(str(tmp_path / "libfastmm_amd.so"))
+
+
+def test_torch_extension_registers_the_operator_schemas() -> None:
+    """The PyTorch-ROCm extension (csrc/torch_ops.cpp) keeps the reference's operator
+    schemas (src/rdna3_fastmm/linear.py:50-167) and one stage operator per entry point."""
+    import torch
+
+    from rdna3_fastmm import _torch_ops  # noqa: F401  (loads libfastmm_torch.so)
+
+    for name in ("linear", "linear_rank7", "linear_rank48"):
+        schema = str(getattr(torch.ops.rdna3_fastmm, name).default._schema)
+        assert schema == f"rdna3_fastmm::{name}(Tensor input, Tensor weight, Tensor? bias=None) -> Tensor"
+    stages = {
+        "left_transform": "(int scheme, Tensor input, Tensor(a!) output, int rows, int inner) -> ()",
+        "weight_transform": "(int scheme, Tensor weight, Tensor(a!) output, int columns, int inner) -> ()",
+        "right_transform": "(int scheme, Tensor right, Tensor(a!) output, int inner, int columns) -> ()",
+        "reconstruct": "(int scheme, Tensor products, Tensor? bias, Tensor(a!) output, int rows, int columns) -> ()",
+    }
+    for name, signature in stages.items():
+        assert str(getattr(torch.ops.rdna3_fastmm_hip, name).default._schema) == f"rdna3_fastmm_hip::{name}{signature}"
+    assert "Tensor(a!) products" in str(torch.ops.rdna3_fastmm_hip.leaf_products.default._schema)
+
+
+@pytest.mark.parametrize(
+    ("shapes", "dtypes", "message"),
+    (
+        (((4, 3), (5, 3)), ("bfloat16", "float16"), "needs bf16 or fp16 input and weight of one dtype"),
+        (((4, 3), (5, 3)), ("float32", "float32"), "needs bf16 or fp16 input and weight of one dtype"),
+        (((4, 3), (5, 3)), ("bfloat16", "bfloat16"), "needs input and weight on one ROCm device"),
+    ),
+)
+def test_torch_operators_reject_bad_operands_before_any_launch(shapes, dtypes, message) -> None:
+    import torch
+
+    from rdna3_fastmm import _torch_ops
+
+    x = torch.zeros(shapes[0], dtype=getattr(torch, dtypes[0]))
+    w = torch.zeros(shapes[1], dtype=getattr(torch, dtypes[1]))
+    for op in (_torch_ops.linear, _torch_ops.linear_rank7, _torch_ops.linear_rank48):
+        with pytest.raises(ValueError, match=message):
+            op(x, w)
