@@ -36,7 +36,12 @@ How each function is pinned (tests/test_oracle.py):
 * ``load_oracle_scheme`` / ``evaluate_program``: exact Brent identity over
   Fractions; the reference's own counts and digests (tests/test_slp.py:17-55,
   tests/test_fastmm_certificate.py:31-33 of the reference); the W-circuit
-  semantics check of tests/test_generate_triton_scheme.py:47-98.
+  semantics check of tests/test_generate_triton_scheme.py:47-98. The fp32
+  association order of every sum: bit-equal to fixed vectors of the
+  reference's generated Triton transforms (``generated/rank{7,48,49,343}_*.py``,
+  read as text by ``tests/golden/make_association_vectors.py``), on inputs
+  that span 21 binades, with a planted regrouping caught
+  (tests/test_association_order.py).
 * ``linear`` / ``matmul`` end to end: the exact small-integer known answer
   (reference tests/test_rdna3.py:406-430) for all three schemes, the fp64
   closed form ``x @ W.T`` on random inputs, and a planted sign error that
