@@ -208,7 +208,8 @@ def leaf_kernel_name(rank: int, mb: int, kb: int, nb: int, compute: str, cus: in
     main = tiles - tail if split_tail and split >= 2 else tiles
     extra = " + thin_rows_kernel for the last tile row" if thin else ""
     if main > cus // 8 * 8 and kb >= 256 and mb * nb * 2 <= 2**31 - 1:
-        return f"fastmm::mfma16::persistent_kernel<{compute}, {compute}> (fastmm_leaf_products){extra}"
+        stream = "true" if rank * mb * nb * 2 > 2**30 else "false"  # products stored non-temporally
+        return f"fastmm::mfma16::persistent_kernel<{compute}, {compute}, {stream}> (fastmm_leaf_products){extra}"
     return f"fastmm::mfma16::leaf_gemm_kernel<{compute}, {compute}> (fastmm_leaf_products){extra}"
 
 

@@ -658,6 +658,11 @@ constexpr int STAGE_ROWS = 64;
 constexpr int PERSISTENT_LDS_BYTES = RING_BYTES + STAGE_ROWS * kTile * 2;  // 160 KB
 constexpr int kStoresPerTile = 32;  // per wave: 4 chunks x 8 passes
 
+// Cache-policy operand of the product stores when kStreamOut is set: the
+// non-temporal bit (nt, bit 1 on gfx950), so products that cannot stay cached
+// until the recombination reads them do not displace operand lines.
+constexpr int kStoreNonTemporal = 2;
+
 // Persistent workgroup wg of `grid` (a multiple of 8): tiles first,
 // first + stride, ... (count of them) of its XCD's range, stride = grid / 8.
 __device__ __forceinline__ void persistent_tiles(int wg, int grid, int total, int& first, int& stride,
@@ -687,7 +692,7 @@ __device__ __forceinline__ unsigned pack2(float lo, float hi) {
   }
 }
 
-template <int kIn, int kOut>
+template <int kIn, int kOut, bool kStreamOut>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void persistent_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B, uint16_t* __restrict__ P,
                        int Mb, int Nb, int Kb, int tiles_m, int tiles_n, int total_tiles) {
@@ -952,7 +957,7 @@ void persistent_kernel(const half_t* __restrict__ A, const half_t* __restrict__ 
         // which the launcher checks)
         const unsigned base = (row0 < mb_u && n0 < nb_u) ? (row0 * nb_u + n0) * 2 : 0u;
         __builtin_amdgcn_raw_buffer_store_b128(staged[h], p_rsrc, inside ? lane_offset : kOutOfRange,
-                                               static_cast<int>(base), 0);
+                                               static_cast<int>(base), kStreamOut ? kStoreNonTemporal : 0);
       }
       asm volatile("" ::: "memory");
     }
@@ -1376,15 +1381,19 @@ int launch_mfma16(const void* a, const void* b, void* p, int64_t rank, int64_t m
   // reservation granted; otherwise one workgroup per tile).
   bool persistent = false;
   if constexpr (kOut != kFP32) {
-    static std::atomic<uint64_t> persistent_granted{0}, persistent_refused{0};
+    // Products beyond 1 GiB (four times the Infinity Cache) are stored with the
+    // non-temporal hint. Measured on the C2-C5 leaf problems: 2.0 GB of
+    // products (K = 1024) -3 % leaf time; 0.40 GB +3 %; 0.13-0.23 GB no change.
+    const bool stream_out = rank * mb * nb * 2 > (int64_t{1} << 30);
+    static std::atomic<uint64_t> persistent_granted[2], persistent_refused[2];
+    auto* kernel = stream_out ? mfma16::persistent_kernel<kIn, kOut, true> : mfma16::persistent_kernel<kIn, kOut, false>;
     const int64_t grid = compute_units() / 8 * 8;
     persistent = grid >= 8 && plan.main_tiles > grid && kb >= 8 * mfma16::BK && mb * nb * 2 <= INT32_MAX &&
-                 try_reserve_lds(mfma16::persistent_kernel<kIn, kOut>, mfma16::PERSISTENT_LDS_BYTES,
-                                 persistent_granted, persistent_refused);
+                 try_reserve_lds(kernel, mfma16::PERSISTENT_LDS_BYTES, persistent_granted[stream_out],
+                                 persistent_refused[stream_out]);
     if (persistent) {
-      mfma16::persistent_kernel<kIn, kOut>
-          <<<dim3(static_cast<unsigned>(grid)), kGemmThreads, mfma16::PERSISTENT_LDS_BYTES, stream>>>(
-              A, B, static_cast<uint16_t*>(p), M, N, K, TM, TN, static_cast<int>(plan.main_tiles));
+      kernel<<<dim3(static_cast<unsigned>(grid)), kGemmThreads, mfma16::PERSISTENT_LDS_BYTES, stream>>>(
+          A, B, static_cast<uint16_t*>(p), M, N, K, TM, TN, static_cast<int>(plan.main_tiles));
       if (int status = check_launch("leaf products")) return status;
     }
   }

@@ -210,7 +210,15 @@ __device__ __forceinline__ Vec<EPT> load_product(const void* products, int64_t o
   }
 }
 
-template <class S, int kProd, int kOut, int EPT, bool kVector, bool kBias>
+// The output is stored with streaming stores: it is written once, and kept out
+// of the caches it leaves them to the next call's transform input (C4: that
+// transform 0.113 ms after this kernel against 0.145 ms after plain stores).
+// kStreamIn: the vector path's product loads stream too; the launcher sets it
+// when the products exceed the Infinity Cache, which then cannot still hold
+// the leaf GEMM's freshly written products (C4's 2.0 GB of products
+// recombine in 0.441 ms streamed, 0.496 ms plain; 0.13-0.23 GB, which stay
+// cached, recombine 3-10 % slower streamed).
+template <class S, int kProd, int kOut, int EPT, bool kVector, bool kBias, bool kStreamIn = false>
 __global__ __launch_bounds__(block_threads<S>()) void reconstruct_kernel(
     const void* __restrict__ products, const uint16_t* __restrict__ bias,
     uint16_t* __restrict__ out, int64_t rows, int64_t cols, int64_t rows_b, int64_t cols_b) {
@@ -231,7 +239,14 @@ __global__ __launch_bounds__(block_threads<S>()) void reconstruct_kernel(
     const uint16_t* base = static_cast<const uint16_t*>(products) + first;
     Raw raw[S::kRank];
 #pragma unroll
-    for (int r = 0; r < S::kRank; ++r) raw[r] = *reinterpret_cast<const Raw*>(base + static_cast<int64_t>(r) * plane);
+    for (int r = 0; r < S::kRank; ++r) {
+      const uint16_t* at = base + static_cast<int64_t>(r) * plane;
+      if constexpr (kStreamIn) {
+        raw[r] = load_raw16_stream<EPT>(at);
+      } else {
+        raw[r] = *reinterpret_cast<const Raw*>(at);
+      }
+    }
     Raw bias_raw[kBias ? s : 1];
     if constexpr (kBias) {
 #pragma unroll
@@ -244,7 +259,7 @@ __global__ __launch_bounds__(block_threads<S>()) void reconstruct_kernel(
       if (out_row >= rows) return;
       const int64_t out_col = (c % s) * cols_b + col;
       if constexpr (kBias) v = v + raw_to_vec<kOut, EPT>(bias_raw[c % s]);
-      store_vec<kOut, EPT>(out + out_row * cols + out_col, v);
+      store_vec<kOut, EPT, true>(out + out_row * cols + out_col, v);
     };
     S::template output<Vec<EPT>>(load, store);
     return;
@@ -263,7 +278,7 @@ __global__ __launch_bounds__(block_threads<S>()) void reconstruct_kernel(
         const Vec<EPT> b = load_vec<kOut, EPT>(bias + out_col);
         v = v + b;
       }
-      store_vec<kOut, EPT>(p, v);
+      store_vec<kOut, EPT, true>(p, v);
     } else {
 #pragma unroll
       for (int e = 0; e < EPT; ++e) {
@@ -526,14 +541,25 @@ int launch_transposed(int dtype, int plane_dtype, const void* src, void* dst, in
   return check_launch("right transform");
 }
 
+// Products larger than this stream past the caches in the recombination: the
+// MI355X Infinity Cache holds 256 MiB.
+constexpr int64_t kStreamProductBytes = int64_t{256} << 20;
+
 template <class S, int kProd, int kOut, bool kBias>
 void launch_reconstruct_typed(bool vector, dim3 grid, hipStream_t stream, const void* products,
                               const uint16_t* bias, uint16_t* out, int64_t rows, int64_t cols,
                               int64_t rows_b, int64_t cols_b) {
   constexpr int W = reconstruct_width<S, kProd>();
   if (vector) {
-    reconstruct_kernel<S, kProd, kOut, W, true, kBias>
-        <<<grid, block_threads<S>(), 0, stream>>>(products, bias, out, rows, cols, rows_b, cols_b);
+    constexpr bool kCanStream = kProd != kFP32 && S::kRank <= 64;  // the raw-bits load path
+    const int64_t product_bytes = static_cast<int64_t>(S::kRank) * rows_b * cols_b * 2;
+    if (kCanStream && product_bytes > kStreamProductBytes) {
+      reconstruct_kernel<S, kProd, kOut, W, true, kBias, kCanStream>
+          <<<grid, block_threads<S>(), 0, stream>>>(products, bias, out, rows, cols, rows_b, cols_b);
+    } else {
+      reconstruct_kernel<S, kProd, kOut, W, true, kBias>
+          <<<grid, block_threads<S>(), 0, stream>>>(products, bias, out, rows, cols, rows_b, cols_b);
+    }
   } else {
     reconstruct_kernel<S, kProd, kOut, 1, false, kBias>
         <<<grid, block_threads<S>(), 0, stream>>>(products, bias, out, rows, cols, rows_b, cols_b);
