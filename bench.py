@@ -194,22 +194,36 @@ def leaf_kernel_name(rank: int, mb: int, kb: int, nb: int, compute: str, cus: in
     the persistent kernel when the tiles left after the split-K tail exceed one round
     (CUs rounded down to a multiple of 8), Kb >= 256 and a leaf's products fit 32-bit
     offsets; else one workgroup per tile; the 32x32x16 kernel for other Kb. A last tile
-    row of at most 16 rows goes to fastmm::thin::thin_rows_kernel when that takes the
-    256x256 tiles down a round and R * Nb <= 32768."""
+    row of at most 16 rows is left out of the 256x256 tiles when that takes them down a
+    round: fused into the persistent kernel (its strip form) when those tiles have no
+    split-K tail and the last group of 8 tile rows holds at least 4, else run by
+    fastmm::thin::thin_rows_kernel when R * Nb <= 32768."""
     if kb % 128:
         return f"fastmm::fast::leaf_gemm_kernel<{compute}, {compute}> (fastmm_leaf_products)"
     tiles_n = -(-nb // 256)
     with_row = rank * -(-mb // 256) * tiles_n
-    thin = (mb > 256 and 0 < mb % 256 <= 16 and rank * nb <= 32768
-            and -(-(with_row - rank * tiles_n) // cus) < -(-with_row // cus))
-    tiles = with_row - rank * tiles_n if thin else with_row
-    tail = tiles % cus
-    split = min(8, kb // 128, 3 * cus // (4 * tail)) if tail else 0
+    without = with_row - rank * tiles_n
+
+    def split_of(tiles: int) -> tuple[int, int]:
+        tail = tiles % cus
+        split = min(8, kb // 128, 3 * cus // (4 * tail)) if tail else 0
+        return tail, split
+
+    drop = mb > 256 and 0 < mb % 256 <= 16 and -(-without // cus) < -(-with_row // cus)
+    full = mb // 256
+    strip = drop and full - 8 * ((full - 1) // 8) >= 4 and split_of(without)[1] < 2
+    thin = drop and not strip and rank * nb <= 32768
+    tiles = without if strip or thin else with_row
+    tail, split = split_of(tiles)
     main = tiles - tail if split_tail and split >= 2 else tiles
     extra = " + thin_rows_kernel for the last tile row" if thin else ""
     if main > cus // 8 * 8 and kb >= 256 and mb * nb * 2 <= 2**31 - 1:
         stream = "true" if rank * mb * nb * 2 > 2**30 else "false"  # products stored non-temporally
-        return f"fastmm::mfma16::persistent_kernel<{compute}, {compute}, {stream}> (fastmm_leaf_products){extra}"
+        fused = "true" if strip else "false"  # the last tile row fused as a strip
+        return (f"fastmm::mfma16::persistent_kernel<{compute}, {compute}, {stream}, {fused}> "
+                f"(fastmm_leaf_products){extra}")
+    if strip:
+        extra = " + thin_rows_kernel for the last tile row"
     return f"fastmm::mfma16::leaf_gemm_kernel<{compute}, {compute}> (fastmm_leaf_products){extra}"
 
 

@@ -653,6 +653,19 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
 // stores stay in flight (vmcnt 48 instead of 16): they drain under its MFMAs.
 // The prologue issues 32 stores that write nothing, so every tile starts with
 // the same count of operations in flight.
+//
+// kStrip fuses a last partial tile row of at most 16 rows (the "strip", rows
+// tiles_m * 256 .. Mb - 1) into the tiles of the last group of 8 tile rows,
+// while their B' slices are in LDS: a separate pass over the strip would
+// re-read all of B' from memory. Tile (tm, tn) at position p = tm - (first
+// row of the group) gives wave w the strip's 16-column block b = 4 p + w of
+// tile column tn (b >= 16 or past Nb: no work). Per slice each wave issues one
+// more MFMA (B' rows 16 b .. 16 b + 15 of the tile, read from LDS, against
+// the strip's A' rows), one more LDS fragment read and one more load (the
+// strip's A' fragment, straight into registers, four slices ahead like the
+// ring); waves without work run the MFMA on zeros and store nothing. Per tile
+// each wave issues one more (8-byte) store. So every step has 9 loads and
+// every tile 33 stores, and the waits scale to match.
 constexpr int RING_BYTES = STAGES * STAGE_HALVES * 2;                      // 128 KB
 constexpr int STAGE_ROWS = 64;
 constexpr int PERSISTENT_LDS_BYTES = RING_BYTES + STAGE_ROWS * kTile * 2;  // 160 KB
@@ -692,7 +705,7 @@ __device__ __forceinline__ unsigned pack2(float lo, float hi) {
   }
 }
 
-template <int kIn, int kOut, bool kStreamOut>
+template <int kIn, int kOut, bool kStreamOut, bool kStrip>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void persistent_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B, uint16_t* __restrict__ P,
                        int Mb, int Nb, int Kb, int tiles_m, int tiles_n, int total_tiles) {
@@ -704,6 +717,17 @@ void persistent_kernel(const half_t* __restrict__ A, const half_t* __restrict__ 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
+  // vmcnt budget of the step waits: two steps of loads (the slice two ahead
+  // resident), plus a tile's stores in a tile's first two steps
+  constexpr int kLoadsPerStep = kStrip ? 9 : 8;
+  constexpr int kStoresPerWave = kStoresPerTile + (kStrip ? 1 : 0);
+  constexpr int kWaitSteady = 2 * kLoadsPerStep, kWaitFirst = kStoresPerWave + 2 * kLoadsPerStep;
+  // the strip's first tile row of the last group, and the strip block of this
+  // wave in tile row tm (>= 16: none)
+  const int strip_group = 8 * ((tiles_m - 1) / 8);
+  auto strip_block = [&](int tm) __attribute__((always_inline)) {
+    return tm >= strip_group ? 4 * (tm - strip_group) + wave : 16;
+  };
 
   // Load descriptor of the tile whose slices are being fetched (as in
   // leaf_gemm_kernel; logical < 0: no tile, every lane out of range, so the
@@ -714,6 +738,7 @@ void persistent_kernel(const half_t* __restrict__ A, const half_t* __restrict__ 
       static_cast<unsigned>(((wave * 16 + (lane >> 2)) * kSlab + ((lane & 3) ^ ((lane >> 4) & 3)) * 8) * 2);
   __amdgpu_buffer_rsrc_t a_rsrc, b_rsrc;
   unsigned a_off[SEGMENTS], b_off[SEGMENTS];
+  unsigned r_off = kOutOfRange;  // the strip's A' fragment (kStrip)
   auto set_loads = [&](int logical) __attribute__((always_inline)) {
     const bool none = logical < 0;
     int leaf, tm, tn;
@@ -732,6 +757,14 @@ void persistent_kernel(const half_t* __restrict__ A, const half_t* __restrict__ 
       a_off[q] = a < a_limit ? a : kOutOfRange;
       b_off[q] = b < b_limit ? b : kOutOfRange;
     }
+    if constexpr (kStrip) {
+      // this wave's strip A' fragment: row tiles_m * 256 + lane % 16, 8-wide K
+      // chunk lane / 16 of each slab (rows past the leaf, or no block: zeros)
+      const int block = strip_block(tm);
+      const int row = tiles_m * kTile + (lane & 15);
+      const bool active = !none && block < 16 && tn * kTile + 16 * block < Nb && row < Mb;
+      r_off = active ? static_cast<unsigned>((row * kSlab + (lane >> 4) * 8) * 2) : kOutOfRange;
+    }
   };
 
   const int fr = lane & 15, fc = lane >> 4;
@@ -745,6 +778,30 @@ void persistent_kernel(const half_t* __restrict__ A, const half_t* __restrict__ 
 
   half8 fa[2][FM], fb[2][FN];
   float4v acc[FM][FN];  // never zeroed: a tile's first MFMAs take srcC = 0
+  // kStrip: the strip block's B' fragment (a set per slice parity, from LDS),
+  // the strip A' fragments (a ring of four slices, from memory) and the
+  // strip's accumulator (VGPRs; the AGPRs hold acc)
+  half8 fx[2] = {half8{}, half8{}};
+  uint4v rfrag[STAGES] = {};
+  float4v acc_x = {};
+  unsigned base_x[2] = {0u, 0u};
+  // base_x for the tile being computed: LDS rows 16 b + fr of its B' tile
+  // (the B' fragment reads' swizzle; no block: block 15, read and unused)
+  auto set_strip = [&](int logical) __attribute__((always_inline)) {
+    if constexpr (kStrip) {
+      int leaf, tm, tn;
+      tile_of(logical, tiles_m, tiles_n, 8, leaf, tm, tn);
+      const int block = min(strip_block(tm), 15);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        base_x[h] = (unsigned)(uintptr_t)(lds_ptr)(smem + h * 2 * STAGE_HALVES + kTile * BK + block * 16 * BK + rd);
+      }
+    }
+  };
+  // the strip A' fragment of slice kt of the descriptor's tile into ring slot `slot`
+  auto strip_load = [&](int kt, int slot) __attribute__((always_inline)) {
+    rfrag[slot] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, r_off, kt * Mb * kSlab * 2, 0);
+  };
 #pragma unroll
   for (int s = 0; s < 2; ++s)
 #pragma unroll
@@ -805,10 +862,32 @@ void persistent_kernel(const half_t* __restrict__ A, const half_t* __restrict__ 
 #define FASTMM_TIE(i)                                                                               \
   asm volatile("" : "+a"(acc[i][0]), "+a"(acc[i][1]), "+a"(acc[i][2]), "+a"(acc[i][3]),             \
                     "+a"(acc[i][4]), "+a"(acc[i][5]), "+a"(acc[i][6]), "+a"(acc[i][7]))
+  // The strip MFMA accumulates in VGPRs (early clobber on the first: its
+  // destination must not overlap the sources).
+#define FASTMM_STRIP_MFMA(kSet, kSlot)                                                              \
+  do {                                                                                              \
+    if constexpr (kFirst && kIn == kBF16)                                                           \
+      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0"                                         \
+                   : "=&v"(acc_x) : "v"(fx[kSet]), "v"(rfrag[kSlot]));                              \
+    else if constexpr (kFirst)                                                                      \
+      asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, 0"                                          \
+                   : "=&v"(acc_x) : "v"(fx[kSet]), "v"(rfrag[kSlot]));                              \
+    else if constexpr (kIn == kBF16)                                                                \
+      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"                                        \
+                   : "+v"(acc_x) : "v"(fx[kSet]), "v"(rfrag[kSlot]));                               \
+    else                                                                                            \
+      asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0"                                         \
+                   : "+v"(acc_x) : "v"(fx[kSet]), "v"(rfrag[kSlot]));                               \
+  } while (0)
+#define FASTMM_STRIP_READ(kSlotSrc, kSet)                                                           \
+  asm volatile("ds_read_b128 %0, %1 offset:%2"                                                      \
+               : "+v"(fx[kSet])                                                                     \
+               : "v"(base_x[(kSlotSrc) / 2]), "i"(((kSlotSrc) % 2) * STAGE_HALVES * 2))
   auto fence = [&]() __attribute__((always_inline)) {
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
     FASTMM_TIE(0); FASTMM_TIE(1); FASTMM_TIE(2); FASTMM_TIE(3);
     FASTMM_TIE(4); FASTMM_TIE(5); FASTMM_TIE(6); FASTMM_TIE(7);
+    if constexpr (kStrip) asm volatile("" : "+v"(acc_x));
   };
 
   // One slice in ring slot kSlot (fragments in register set kSlot % 2): kLoad
@@ -829,8 +908,18 @@ void persistent_kernel(const half_t* __restrict__ A, const half_t* __restrict__ 
     FASTMM_GROUP(4); FASTMM_GROUP(5); FASTMM_GROUP(6); FASTMM_GROUP(7);
     FASTMM_GROUP(8); FASTMM_GROUP(9); FASTMM_GROUP(10); FASTMM_GROUP(11);
     FASTMM_GROUP(12); FASTMM_GROUP(13); FASTMM_GROUP(14); FASTMM_GROUP(15);
-    if constexpr (kWait == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-    else if constexpr (kWait == 48) asm volatile("s_waitcnt vmcnt(48)" ::: "memory");
+    if constexpr (kStrip) {
+      // the strip block: this slice's MFMA, then the next slice's B' fragment
+      // and (after the MFMA has read it) a refill of this ring slot's A' one
+      FASTMM_STRIP_MFMA(kSet, kSlot);
+      if constexpr (kNext) FASTMM_STRIP_READ(kNextSlot, 1 - kSet);
+      if constexpr (kLoad) strip_load(load_kt, kSlot);
+    }
+    static_assert(kWait == 16 || kWait == 48, "steady (16) or tile-start (48) wait");
+    if constexpr (kWait == 16 && kWaitSteady == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    else if constexpr (kWait == 16 && kWaitSteady == 18) asm volatile("s_waitcnt vmcnt(18)" ::: "memory");
+    else if constexpr (kWait == 48 && kWaitFirst == 48) asm volatile("s_waitcnt vmcnt(48)" ::: "memory");
+    else if constexpr (kWait == 48 && kWaitFirst == 51) asm volatile("s_waitcnt vmcnt(51)" ::: "memory");
     else static_assert(kWait < 0, "unsupported vmcnt");
     if constexpr (kNext) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     fast::barrier();
@@ -869,6 +958,7 @@ void persistent_kernel(const half_t* __restrict__ A, const half_t* __restrict__ 
     FASTMM_READ(kSrc, kDst, 4); FASTMM_READ(kSrc, kDst, 5); FASTMM_READ(kSrc, kDst, 6); FASTMM_READ(kSrc, kDst, 7);
     FASTMM_READ(kSrc, kDst, 8); FASTMM_READ(kSrc, kDst, 9); FASTMM_READ(kSrc, kDst, 10); FASTMM_READ(kSrc, kDst, 11);
     FASTMM_READ(kSrc, kDst, 12); FASTMM_READ(kSrc, kDst, 13); FASTMM_READ(kSrc, kDst, 14); FASTMM_READ(kSrc, kDst, 15);
+    if constexpr (kStrip) FASTMM_STRIP_READ(kSrc, kDst);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     fast::barrier();
   };
@@ -876,20 +966,26 @@ void persistent_kernel(const half_t* __restrict__ A, const half_t* __restrict__ 
   const unsigned stage_base = (unsigned)(uintptr_t)(lds_ptr)(smem) + RING_BYTES;
   set_loads(first);
 #pragma unroll
-  for (int s = 0; s < STAGES; ++s)
+  for (int s = 0; s < STAGES; ++s) {
 #pragma unroll
     for (int idx = 0; idx < 8; ++idx) load_one(s, s, idx);
+    if constexpr (kStrip) strip_load(s, s);
+  }
   {
     // stores that write nothing (no records), in the place of a previous tile's
     const __amdgpu_buffer_rsrc_t none = __builtin_amdgcn_make_buffer_rsrc(P, 0, 0, 0x00020000);
     asm volatile("" ::: "memory");
 #pragma unroll
-    for (int q = 0; q < kStoresPerTile; ++q)
+    for (int q = 0; q < kStoresPerWave; ++q)
       __builtin_amdgcn_raw_buffer_store_b128(uint4v{0, 0, 0, 0}, none, kOutOfRange, 0, 0);
     asm volatile("" ::: "memory");
   }
-  asm volatile("s_waitcnt vmcnt(48)" ::: "memory");  // slices 0 and 1 resident
+  // slices 0 and 1 resident
+  if constexpr (kWaitFirst == 48) asm volatile("s_waitcnt vmcnt(48)" ::: "memory");
+  else if constexpr (kWaitFirst == 51) asm volatile("s_waitcnt vmcnt(51)" ::: "memory");
+  else static_assert(kWaitFirst < 0, "unsupported vmcnt");
   fast::barrier();
+  set_strip(first);
   read_first_slice();
 
   for (int t = 0; t < count; ++t) {
@@ -961,6 +1057,19 @@ void persistent_kernel(const half_t* __restrict__ A, const half_t* __restrict__ 
       }
       asm volatile("" ::: "memory");
     }
+    if constexpr (kStrip) {
+      // this wave's strip block: lane l holds row tiles_m * 256 + l % 16,
+      // columns 16 b + 4 (l / 16) .. + 3 of the tile (8 bytes)
+      const int block = strip_block(tm);
+      const unsigned row = static_cast<unsigned>(tiles_m * kTile) + er;
+      const unsigned col = tn * kTile + 16 * static_cast<unsigned>(block) + 4 * eg;
+      const bool inside = block < 16 && row < mb_u && col < nb_u;  // Nb % 8 == 0: all 4 columns or none
+      const uint2v v = {pack2<kOut>(acc_x[0], acc_x[1]), pack2<kOut>(acc_x[2], acc_x[3])};
+      __builtin_amdgcn_raw_buffer_store_b64(v, p_rsrc, inside ? (row * nb_u + col) * 2 : kOutOfRange, 0,
+                                            kStreamOut ? kStoreNonTemporal : 0);
+      asm volatile("" ::: "memory");
+      if (t + 1 < count) set_strip(logical + stride);
+    }
     read_first_slice();
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last (empty) refills have landed in LDS
@@ -968,6 +1077,8 @@ void persistent_kernel(const half_t* __restrict__ A, const half_t* __restrict__ 
 #undef FASTMM_MFMA
 #undef FASTMM_GROUP
 #undef FASTMM_TIE
+#undef FASTMM_STRIP_MFMA
+#undef FASTMM_STRIP_READ
 }
 
 }  // namespace mfma16
@@ -1260,19 +1371,32 @@ int64_t tail_scratch_bytes(const TailSplit& plan) {
 constexpr int64_t kThinMaxRankColumns = 32768;
 
 struct LeafPlan {
-  int64_t tiles_m, tiles_n;  // 256 x 256 tiles (the thin row excluded)
-  bool thin;
+  int64_t tiles_m, tiles_n;  // 256 x 256 tiles (the thin row or strip excluded)
+  bool thin;   // the last (partial) tile row by thin_rows_kernel
+  bool strip;  // the last (partial) tile row fused into the persistent kernel
   TailSplit split;
 };
 
+// A last tile row of at most 16 rows is left out of the tiles when that takes
+// them down a round. It then goes into the persistent kernel as a strip when
+// the tiles have no split-K tail and the last group of 8 tile rows has at
+// least 4 (one strip block per wave and tile covers its 16 blocks); the
+// launcher runs thin_rows_kernel over it when the persistent kernel is not
+// used. Otherwise thin_rows_kernel takes it if the strip is cheap there.
 LeafPlan leaf_plan(int64_t rank, int64_t mb, int64_t kb, int64_t nb) {
   const int64_t rem = mb % kTile, tiles_n = ceil_div(nb, kTile);
   const int64_t with_row = ceil_div(mb, kTile) * tiles_n * rank, without_row = with_row - tiles_n * rank;
   const int64_t cus = compute_units();
-  const bool thin = mb > kTile && rem > 0 && rem <= thin::kRows && rank * nb <= kThinMaxRankColumns && cus > 0 &&
+  const bool drop = mb > kTile && rem > 0 && rem <= thin::kRows && cus > 0 &&
                     ceil_div(without_row, cus) < ceil_div(with_row, cus);
+  if (drop) {
+    const int64_t full = mb / kTile, last_group = full - 8 * ((full - 1) / 8);
+    const TailSplit split = tail_split(without_row, kb);
+    if (last_group >= 4 && split.tail == 0) return {full, tiles_n, false, true, split};
+  }
+  const bool thin = drop && rank * nb <= kThinMaxRankColumns;
   const int64_t tiles_m = ceil_div(mb, kTile) - (thin ? 1 : 0);
-  return {tiles_m, tiles_n, thin, tail_split(rank * tiles_m * tiles_n, kb)};
+  return {tiles_m, tiles_n, thin, false, tail_split(rank * tiles_m * tiles_n, kb)};
 }
 
 // ---------------------------------------------------------------- launchers
@@ -1385,12 +1509,18 @@ int launch_mfma16(const void* a, const void* b, void* p, int64_t rank, int64_t m
     // non-temporal hint. Measured on the C2-C5 leaf problems: 2.0 GB of
     // products (K = 1024) -3 % leaf time; 0.40 GB +3 %; 0.13-0.23 GB no change.
     const bool stream_out = rank * mb * nb * 2 > (int64_t{1} << 30);
-    static std::atomic<uint64_t> persistent_granted[2], persistent_refused[2];
-    auto* kernel = stream_out ? mfma16::persistent_kernel<kIn, kOut, true> : mfma16::persistent_kernel<kIn, kOut, false>;
+    const int variant = (stream_out ? 1 : 0) + (layout.strip ? 2 : 0);
+    static std::atomic<uint64_t> persistent_granted[4], persistent_refused[4];
+    decltype(&mfma16::persistent_kernel<kIn, kOut, false, false>) const kernels[4] = {
+                              mfma16::persistent_kernel<kIn, kOut, false, false>,
+                              mfma16::persistent_kernel<kIn, kOut, true, false>,
+                              mfma16::persistent_kernel<kIn, kOut, false, true>,
+                              mfma16::persistent_kernel<kIn, kOut, true, true>};
+    auto* kernel = kernels[variant];
     const int64_t grid = compute_units() / 8 * 8;
     persistent = grid >= 8 && plan.main_tiles > grid && kb >= 8 * mfma16::BK && mb * nb * 2 <= INT32_MAX &&
-                 try_reserve_lds(kernel, mfma16::PERSISTENT_LDS_BYTES, persistent_granted[stream_out],
-                                 persistent_refused[stream_out]);
+                 try_reserve_lds(kernel, mfma16::PERSISTENT_LDS_BYTES, persistent_granted[variant],
+                                 persistent_refused[variant]);
     if (persistent) {
       kernel<<<dim3(static_cast<unsigned>(grid)), kGemmThreads, mfma16::PERSISTENT_LDS_BYTES, stream>>>(
           A, B, static_cast<uint16_t*>(p), M, N, K, TM, TN, static_cast<int>(plan.main_tiles));
@@ -1412,7 +1542,7 @@ int launch_mfma16(const void* a, const void* b, void* p, int64_t rank, int64_t m
         static_cast<const float*>(scratch), p, M, N, TM, TN, base, split);
     if (int status = check_launch("leaf products (tail reduction)")) return status;
   }
-  if (layout.thin) {
+  if (layout.thin || (layout.strip && !persistent)) {
     thin::thin_rows_kernel<kIn, kOut>
         <<<dim3(static_cast<unsigned>(ceil_div(nb, thin::kCols)), static_cast<unsigned>(rank)), kGemmThreads, 0,
            stream>>>(A, B, p, M, N, K, static_cast<int>(tiles_m * kTile));

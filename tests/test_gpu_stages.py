@@ -258,23 +258,30 @@ def test_leaf_products_within_fp32_accumulation_bound(dims, operand_dtype, produ
 def test_leaf_scratch_sizes_follow_the_tail_plan() -> None:
     """The split-K tail plan: with one 256x256 tile per CU per round, a last round of
     `tail = tiles % CUs` tiles is split along K into min(8, Kb // 128, 3*CUs // (4*tail))
-    parts (none below 2), each a 256 KB fp32 tile of scratch. A last tile row that runs
-    in the thin-row kernel is not counted."""
+    parts (none below 2), each a 256 KB fp32 tile of scratch. A last tile row of at
+    most 16 rows is left out when that takes the tiles down a round: as a strip fused
+    into the persistent kernel (tiles without a split tail, a last group of 8 tile rows
+    holding at least 4), else in the thin-row kernel when rank * Nb <= 32768."""
     cus = torch.cuda.get_device_properties(DEVICE).multi_processor_count
 
-    def expected(rank, mb, kb, nb):
-        # a last tile row of at most 16 rows (below a full one) runs in its own kernel
-        # when that takes the tiles down a round and rank * Nb <= 32768
-        tiles_n = -(-nb // 256)
-        tiles = rank * -(-mb // 256) * tiles_n
-        if (mb > 256 and 0 < mb % 256 <= 16 and rank * nb <= 32768
-                and -(-(tiles - rank * tiles_n) // cus) < -(-tiles // cus)):
-            tiles -= rank * tiles_n
+    def tail_bytes(tiles, kb):
         tail = tiles % cus
         if tail == 0:
             return 0
         split = min(8, kb // 128, 3 * cus // (4 * tail))
         return tail * split * 256 * 256 * 4 if split >= 2 else 0
+
+    def expected(rank, mb, kb, nb):
+        tiles_n = -(-nb // 256)
+        with_row = rank * -(-mb // 256) * tiles_n
+        without = with_row - rank * tiles_n
+        if mb > 256 and 0 < mb % 256 <= 16 and -(-without // cus) < -(-with_row // cus):
+            full = mb // 256
+            if full - 8 * ((full - 1) // 8) >= 4 and tail_bytes(without, kb) == 0:
+                return 0  # the strip
+            if rank * nb <= 32768:
+                return tail_bytes(without, kb)  # the thin-row kernel
+        return tail_bytes(with_row, kb)
 
     # C3 (tail 47), C2 (64), whole rounds, one tile, K too short, split capped by
     # Kb, a tail of 128 (no split), 24 (split 8), 16 (capped at 8)
@@ -329,17 +336,29 @@ def test_persistent_and_per_tile_kernels_agree_bitwise(rank, mb, kb, nb, scale, 
 @pytest.mark.parametrize(
     ("rank", "mb", "kb", "nb", "dtype", "product_dtype"),
     (
-        (7, 4107, 1024, 2304, torch.float16, torch.float16),  # C3's 11-row edge
-        (2, 2320, 256, 3320, torch.float16, torch.float16),  # 16 rows, ragged columns, 8 slices
+        # the strip fused into the persistent kernel: C3's 11-row edge, rank 48 at C3
+        # (6 rows; 8 and 16 slices), a last group of 4 tile rows with ragged columns,
+        # 16 rows and 1 row, bf16
+        (7, 4107, 1024, 2304, torch.float16, torch.float16),
+        (48, 2054, 256, 1152, torch.float16, torch.float16),
+        (48, 2054, 512, 1152, torch.float16, torch.float16),
+        (5, 3077, 256, 2040, torch.float16, torch.float16),
+        (7, 4112, 384, 2304, torch.float16, torch.float16),
+        (7, 4097, 512, 2304, torch.bfloat16, torch.bfloat16),
+        # the thin-row kernel: fp32 products (no persistent kernel), a last group of one
+        # tile row (16 rows, ragged columns, 8 slices), one row
+        (7, 4107, 256, 2304, torch.float16, torch.float32),
+        (2, 2320, 256, 3320, torch.float16, torch.float16),
         (2, 2320, 512, 3328, torch.bfloat16, torch.bfloat16),
-        (2, 2305, 384, 3328, torch.float16, torch.float32),  # one row, fp32 products
+        (2, 2305, 384, 3328, torch.float16, torch.float32),
     ),
 )
 def test_thin_tile_row_matches_full_tiles_bitwise(rank, mb, kb, nb, dtype, product_dtype) -> None:
-    """A last tile row of at most 16 rows runs in the thin-row kernel (when that takes the
-    tiles down a round). Padding the leaves with zero rows until that row holds more than
-    16 rows sends it through the 256x256 kernels instead; zero rows change no other row, and both kernels issue the
-    same MFMA sequence per product, so the real rows agree bit for bit."""
+    """A last tile row of at most 16 rows is left out of the 256x256 tiles when that takes
+    them down a round: fused into the persistent kernel as a strip, or run by the thin-row
+    kernel. Padding the leaves with zero rows until that row holds more than 16 rows
+    sends it through the 256x256 tiles instead; zero rows change no other row, and every
+    path issues the same MFMA sequence per product, so the real rows agree bit for bit."""
     print(f"\n[case] thin tile row {(rank, mb, kb, nb)} {dtype} -> {product_dtype}", flush=True)
     cus = torch.cuda.get_device_properties(DEVICE).multi_processor_count
     tiles_n = -(-nb // 256)

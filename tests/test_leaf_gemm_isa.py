@@ -43,6 +43,10 @@ def test_every_operand_and_product_variant_is_checked(assembly) -> None:
     names = set(_kernels(assembly))
     for variant in ("ILi1ELi1E", "ILi1ELi2E", "ILi0ELi0E", "ILi0ELi2E"):
         assert any(variant in n for n in names), (variant, names)
+    # the persistent kernel's <stream products, strip> forms, for both 16-bit types
+    for operand in ("ILi1ELi1E", "ILi0ELi0E"):
+        for flags in ("Lb0ELb0E", "Lb1ELb0E", "Lb0ELb1E", "Lb1ELb1E"):
+            assert any(f"persistent_kernel{operand}{flags}" in n for n in names), (operand, flags)
 
 
 def test_no_accumulator_access_inside_mfma_latency(assembly) -> None:
@@ -92,12 +96,16 @@ def test_main_loop_shape(assembly) -> None:
             if line.split(";", 1)[0].strip() and not line.strip().startswith(";")
         ]
         count = lambda prefix: sum(op.startswith(prefix) for op in opcodes)  # noqa: E731
-        # four slices per iteration: 64 MFMAs, 16 fragment reads, 8 refills each
+        # four slices per iteration: 64 MFMAs, 16 fragment reads, 8 refills
+        # each; the persistent kernel's strip form (last template argument
+        # true) adds one MFMA, one fragment read and one load per slice
         operand = re.search(r"kernelILi(\d)E", name).group(1)  # first template argument
+        strip = re.search(r"persistent_kernelILi\dELi\dELb[01]ELb([01])E", name)
+        extra = 4 if strip and strip.group(1) == "1" else 0
         mfma = "v_mfma_f32_16x16x32_bf16" if operand == "0" else "v_mfma_f32_16x16x32_f16"
-        assert count(mfma) == 256, name
-        assert count("ds_read_b128") == 64, name
-        assert count("buffer_load_dwordx4") == 32, name
+        assert count(mfma) == 256 + extra, name
+        assert count("ds_read_b128") == 64 + extra, name
+        assert count("buffer_load_dwordx4") == 32 + extra, name
         assert count("s_barrier") == 4, name
         for forbidden in ("v_accvgpr", "scratch_", "v_mov", "global_load", "flat_"):
             assert count(forbidden) == 0, (name, forbidden)
