@@ -1363,11 +1363,14 @@ int64_t tail_scratch_bytes(const TailSplit& plan) {
 
 // The 16x16x32 path's launch plan: the split-K tail is planned on the
 // 256 x 256 tiles, and a last tile row of at most 16 rows (below a full one)
-// goes to thin_rows_kernel when that takes the tiles down a round and the
-// strip is cheap. The strip re-reads all of B' (R * Nb * Kb * 2 bytes), which
-// costs about R * Nb / 64K tile rounds at any Kb: on MI355X it saved 4 % of
-// the leaf stage at R * Nb = 16128 (rank 7, 8214 x 12288 x 4608) and lost
-// 1.4 % at 55296 (rank 48, same shape).
+// is left out of them when that takes the tiles down a round. The persistent
+// kernel's strip form takes it where it applies (leaf_plan): at 8214 x 12288
+// x 4608 that made the leaf stage 1.8 % (rank 7) and 6.2 % (rank 48) faster
+// than the paths below. Otherwise thin_rows_kernel takes it if the strip is
+// cheap there: a separate pass re-reads all of B' (R * Nb * Kb * 2 bytes),
+// about R * Nb / 64K tile rounds at any Kb. It saved 4 % of the leaf stage at
+// R * Nb = 16128 (rank 7, 8214 x 12288 x 4608) and lost 1.4 % at 55296
+// (rank 48, same shape), where the row then runs as whole tiles.
 constexpr int64_t kThinMaxRankColumns = 32768;
 
 struct LeafPlan {
