@@ -2,8 +2,9 @@
 
 The launcher picks the leaf kernel from the block shape: the register-staged
 generic kernel (ragged Kb or Nb), the 32x32x16 kernel (Kb % 32 == 0, Kb >= 96),
-the 16x16x32 kernels (Kb % 128 == 0; persistent beyond one round of tiles), the
-thin last-row kernel (a last tile row of at most 16 rows) and the split-K tail;
+the 16x16x32 kernels (Kb % 128 == 0; persistent beyond one round of tiles), a
+last tile row of at most 16 rows (fused into the persistent kernel as a strip, or
+the thin last-row kernel) and the split-K tail;
 the transforms pick a vector or a scalar path. These shapes cross those
 thresholds for each scheme, plus a seeded random sample. Every case runs the
 dynamic plan, checks its stages against the oracle on a sample of block rows and
@@ -39,6 +40,10 @@ def _threshold_shapes(key: str) -> list[tuple[int, int, int]]:
     # a last tile row of 11 rows that the thin kernel takes (rank x Nb <= 32768, and
     # dropping the row saves a round of 256 x 256 tiles)
     shapes.append({"rank7": (534, 512, 9360), "rank48": (1068, 1024, 2720), "rank49": (1068, 1024, 2656)}[key])
+    # the north star's M = 8214 with a short K: a last tile row of 11 (rank 7) or 6
+    # (rank 48/49) rows below a last group of 8 tile rows, fused into the persistent
+    # kernel as a strip
+    shapes.append((8214, 256 * s, 4608))
     return shapes
 
 
