@@ -3,16 +3,18 @@
 Every stage of a plan is a kernel launch on the current stream with caller-owned
 buffers: no allocation (given ``output``), no host synchronization, no memset. So
 a captured ``run_linear`` / ``run_linear_packed`` replays exactly (bitwise) like
-the eager call on the same inputs. The shapes put the persistent leaf GEMM and
-the split-K tail (rank 7) and a persistent launch with whole rounds (rank 48)
-inside the graph. Each replay follows eager work and a synchronization, and is
-checked on its own.
+the eager call on the same inputs. The shapes put inside the graph the persistent
+leaf GEMM with the split-K tail (rank 7), a persistent launch with whole rounds
+(rank 48), the persistent kernel's strip form for a last tile row of 11 rows
+(rank 7, M = 8214), and products large enough (1.6 GB, rank 49) that the leaf
+GEMM stores and the recombination loads them non-temporally. Each replay follows
+eager work and a synchronization, and is checked on its own.
 """
 
 import pytest
 import torch
 
-from rdna3_fastmm.runtime import Rank7Plan, Rank48Plan
+from rdna3_fastmm.runtime import Rank7Plan, Rank48Plan, Rank49Plan
 
 pytestmark = pytest.mark.gpu
 
@@ -32,6 +34,8 @@ def _tile_plan(plan) -> tuple[int, int]:
         (Rank7Plan, (4608, 1024, 4608), True),  # 567 tiles: persistent rounds + split-K tail
         (Rank7Plan, (4608, 1024, 4608), False),
         (Rank48Plan, (4096, 2048, 4096), True),  # 768 tiles: three whole rounds
+        (Rank7Plan, (8214, 512, 4608), True),  # a last tile row of 11 rows fused as a strip
+        (Rank49Plan, (16384, 1024, 16384), True),  # 1.6 GB of products: streamed stores and loads
     ),
 )
 def test_captured_linear_replays_match_eager(plan_type, shape, packed) -> None:

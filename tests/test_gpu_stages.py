@@ -304,6 +304,7 @@ def test_leaf_scratch_sizes_follow_the_tail_plan() -> None:
         (3, 2304, 1024, 4096, 30.0, torch.float16),  # fp16 overflow to infinity
         (3, 2048, 256, 4096, 1e-3, torch.float16),  # fp16 subnormals; 8 slices, the minimum
         (7, 1000, 384, 2776, 1.0, torch.bfloat16),
+        (40, 4096, 256, 4096, 1.0, torch.float16),  # 1.34 GB of products: stored non-temporally
     ),
 )
 def test_persistent_and_per_tile_kernels_agree_bitwise(rank, mb, kb, nb, scale, dtype) -> None:

@@ -66,6 +66,26 @@ def test_no_alloc_products_equal_the_scratch_entry_point(products_dtype) -> None
     assert needs[0] > needs[1] > 0 and needs[2] == STATIC_SCRATCH_BYTES and needs[3] == needs[4] == 0
 
 
+@pytest.mark.parametrize(
+    "dims",
+    (
+        (7, 4107, 256, 2304),  # a last tile row of 11 rows fused into the persistent kernel
+        (40, 4096, 256, 4096),  # 1.34 GB of products, stored non-temporally
+    ),
+)
+def test_no_alloc_runs_the_strip_and_streamed_forms(dims) -> None:
+    rank, mb, kb, nb = dims
+    print(f"\n[case] no-alloc {dims}", flush=True)
+    a, b = _operands(rank, mb, kb, nb, seed=sum(dims))
+    expected = torch.empty((rank, mb, nb), device=DEVICE, dtype=torch.float16)
+    assert _with_scratch(a, b, expected, rank, mb, kb, nb) == 0
+    got = torch.full((rank, mb, nb), float("nan"), device=DEVICE, dtype=torch.float16)
+    torch.cuda.synchronize()
+    _no_alloc(a, b, got, rank, mb, kb, nb)
+    torch.cuda.synchronize()
+    assert torch.equal(got, expected)
+
+
 def test_no_alloc_allocates_nothing() -> None:
     """No allocation through torch's allocator, and the driver's free memory unchanged
     beyond what the library's own array took on its first use."""
