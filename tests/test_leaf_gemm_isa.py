@@ -85,30 +85,48 @@ def test_checker_on_accumulator_input_written_just_before() -> None:
     assert _build.fence_violations(loaded + "\ts_waitcnt vmcnt(0)\n\ts_nop 3\n" + mfma + tail) == []
 
 
+def _innermost_loops(body: str) -> list[list[str]]:
+    """Opcodes of each innermost loop: a label and the last branch back to it,
+    with no other such loop strictly inside."""
+    lines = body.splitlines()
+    labels = {}
+    for i, line in enumerate(lines):
+        if match := re.match(r"^(\.LBB\w+):", line):
+            labels[match.group(1)] = i
+    loops = {}
+    for j, line in enumerate(lines):
+        match = re.search(r"\bs_c?branch\w*\s+(\.LBB\w+)", line)
+        if match and match.group(1) in labels and labels[match.group(1)] < j:
+            loops[labels[match.group(1)]] = j  # the last branch back closes the loop
+    spans = sorted(loops.items())
+    inner = [(a, b) for a, b in spans if not any(a < a2 and b2 <= b for a2, b2 in spans if (a2, b2) != (a, b))]
+    return [
+        [line.split(";", 1)[0].split()[0] for line in lines[a + 1 : b + 1]
+         if line.split(";", 1)[0].strip() and not line.strip().startswith(";") and not line.strip().endswith(":")]
+        for a, b in inner
+    ]
+
+
 def test_main_loop_shape(assembly) -> None:
     for name, body in _kernels(assembly).items():
-        # the K loop: the whole-tile kernels' only loop, the persistent kernels' inner one
-        loop = re.search(r"; =>\s*This Inner Loop Header.*?s_cbranch_scc[01]", body, re.DOTALL)
-        assert loop, name
-        opcodes = [
-            line.split(";", 1)[0].split()[0]
-            for line in loop.group(0).splitlines()[1:]
-            if line.split(";", 1)[0].strip() and not line.strip().startswith(";")
-        ]
-        count = lambda prefix: sum(op.startswith(prefix) for op in opcodes)  # noqa: E731
-        # four slices per iteration: 64 MFMAs, 16 fragment reads, 8 refills
-        # each; the persistent kernel's strip form (last template argument
-        # true) adds one MFMA, one fragment read and one load per slice
+        # the K loop: four slices per iteration, each 64 MFMAs, 16 fragment reads
+        # and 8 refills; the persistent kernel's strip form adds one MFMA, one
+        # fragment read and one load per slice
         operand = re.search(r"kernelILi(\d)E", name).group(1)  # first template argument
         strip = re.search(r"persistent_kernelILi\dELi\dELb[01]ELb([01])E", name)
         extra = 4 if strip and strip.group(1) == "1" else 0
         mfma = "v_mfma_f32_16x16x32_bf16" if operand == "0" else "v_mfma_f32_16x16x32_f16"
-        assert count(mfma) == 256 + extra, name
-        assert count("ds_read_b128") == 64 + extra, name
-        assert count("buffer_load_dwordx4") == 32 + extra, name
-        assert count("s_barrier") == 4, name
-        for forbidden in ("v_accvgpr", "scratch_", "v_mov", "global_load", "flat_"):
-            assert count(forbidden) == 0, (name, forbidden)
+        shapes = set()
+        for opcodes in _innermost_loops(body):
+            count = lambda prefix: sum(op.startswith(prefix) for op in opcodes)  # noqa: E731
+            if count("v_mfma") == 0:
+                continue
+            shape = (count(mfma), count("ds_read_b128"), count("buffer_load_dwordx4"), count("s_barrier"))
+            assert shape == (256 + extra, 64 + extra, 32 + extra, 4), (name, shape)
+            for forbidden in ("v_accvgpr", "scratch_", "v_mov", "global_load", "flat_", "v_readlane", "v_writelane"):
+                assert count(forbidden) == 0, (name, forbidden)
+            shapes.add(shape[0] - extra)
+        assert shapes == {256}, (name, shapes)
 
 
 def test_thin_row_kernels_touch_no_load_in_flight(assembly) -> None:
