@@ -39,7 +39,10 @@
 // persistent form (one workgroup per CU streaming slices across tile
 // boundaries, see persistent_kernel), and a last partial round of tiles can
 // be split along K into fp32 parts in caller-owned scratch and added by
-// tail_reduce_kernel (the split-K tail, see tail_split and launch_mfma16).
+// tail_reduce_kernel (the split-K tail, see tail_split and launch_mfma16). A
+// last tile row of at most 16 rows runs fused into the persistent kernel (its
+// strip form) or in thin_rows_kernel (see leaf_plan); products beyond 1 GiB
+// are stored with the non-temporal hint.
 //
 // Generic kernel (any Kb, any alignment): 256 x 256 tile, BK = 64, register-
 // staged loads with zero fill, double-buffered LDS; used for small or ragged
