@@ -650,12 +650,13 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
 // leaves through a 32 KB staging area after the 128 KB ring, in four chunks of
 // 64 rows (32 from each half of the tile, so every wave writes every chunk;
 // 16-byte chunks XOR-swizzled by row: conflict-free 8-byte writes), as full
-// 512-byte row segments. Every wave issues exactly 32 16-byte buffer
-// stores per tile (rows or columns past the leaf get an out-of-range offset
-// and write nothing), and the first two waits of the next tile let those
-// stores stay in flight (vmcnt 48 instead of 16): they drain under its MFMAs.
-// The prologue issues 32 stores that write nothing, so every tile starts with
-// the same count of operations in flight.
+// 512-byte row segments (rows or columns past the leaf get an out-of-range
+// offset and write nothing). Every wait leaves at most two steps of loads in
+// flight and nothing else: vmcnt counts stores as well, and a store can
+// complete before older loads (one past the buffer completes at once), so a
+// wait that allowed a tile's stores in flight would not prove that the loads
+// it waits for have landed. A tile's stores therefore drain during the next
+// tile's first slice.
 //
 // kStrip fuses a last partial tile row of at most 16 rows (the "strip", rows
 // tiles_m * 256 .. Mb - 1) into the tiles of the last group of 8 tile rows,
@@ -667,12 +668,11 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
 // the strip's A' rows), one more LDS fragment read and one more load (the
 // strip's A' fragment, straight into registers, four slices ahead like the
 // ring); waves without work run the MFMA on zeros and store nothing. Per tile
-// each wave issues one more (8-byte) store. So every step has 9 loads and
-// every tile 33 stores, and the waits scale to match.
+// each wave issues one more (8-byte) store. So every step has 9 loads, and
+// the waits scale to match.
 constexpr int RING_BYTES = STAGES * STAGE_HALVES * 2;                      // 128 KB
 constexpr int STAGE_ROWS = 64;
 constexpr int PERSISTENT_LDS_BYTES = RING_BYTES + STAGE_ROWS * kTile * 2;  // 160 KB
-constexpr int kStoresPerTile = 32;  // per wave: 4 chunks x 8 passes
 
 // Cache-policy operand of the product stores when kStreamOut is set: the
 // non-temporal bit (nt, bit 1 on gfx950), so products that cannot stay cached
@@ -720,11 +720,10 @@ void persistent_kernel(const half_t* __restrict__ A, const half_t* __restrict__ 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  // vmcnt budget of the step waits: two steps of loads (the slice two ahead
-  // resident), plus a tile's stores in a tile's first two steps
+  // vmcnt bound of every wait: two steps of loads in flight (the ones of the
+  // slices three and four ahead), so every older load has landed
   constexpr int kLoadsPerStep = kStrip ? 9 : 8;
-  constexpr int kStoresPerWave = kStoresPerTile + (kStrip ? 1 : 0);
-  constexpr int kWaitSteady = 2 * kLoadsPerStep, kWaitFirst = kStoresPerWave + 2 * kLoadsPerStep;
+  constexpr int kWaitLoads = 2 * kLoadsPerStep;
   // the strip's first tile row of the last group, and the strip block of this
   // wave in tile row tm (>= 16: none)
   const int strip_group = 8 * ((tiles_m - 1) / 8);
@@ -893,18 +892,22 @@ void persistent_kernel(const half_t* __restrict__ A, const half_t* __restrict__ 
     if constexpr (kStrip) asm volatile("" : "+v"(acc_x));
   };
 
+  // The vmcnt wait of every step and of the prologue (kWaitLoads in flight).
+  auto wait_loads = [&]() __attribute__((always_inline)) {
+    if constexpr (kWaitLoads == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    else if constexpr (kWaitLoads == 18) asm volatile("s_waitcnt vmcnt(18)" ::: "memory");
+    else static_assert(kWaitLoads < 0, "unsupported vmcnt");
+  };
   // One slice in ring slot kSlot (fragments in register set kSlot % 2): kLoad
   // refills the slot with slice load_kt of the descriptor's tile; kNext reads
-  // the next slice's fragments; the wait leaves kWait operations in flight
-  // (16: the loads of the slices three and four ahead; 48: those and a tile's
-  // 32 stores) so that the slice two ahead is resident; kFirst starts the
-  // accumulators.
-  auto step = [&](int load_kt, auto slot_tag, auto load_tag, auto next_tag, auto wait_tag, auto first_tag)
+  // the next slice's fragments; the wait leaves the loads of the slices three
+  // and four ahead in flight, so the slice two ahead is resident; kFirst
+  // starts the accumulators.
+  auto step = [&](int load_kt, auto slot_tag, auto load_tag, auto next_tag, auto first_tag)
       __attribute__((always_inline)) {
     constexpr int kSlot = decltype(slot_tag)::value;
     constexpr bool kLoad = decltype(load_tag)::value;
     constexpr bool kNext = decltype(next_tag)::value;
-    constexpr int kWait = decltype(wait_tag)::value;
     constexpr bool kFirst = decltype(first_tag)::value;
     constexpr int kSet = kSlot % 2, kNextSlot = (kSlot + 1) % STAGES;
     FASTMM_GROUP(0); FASTMM_GROUP(1); FASTMM_GROUP(2); FASTMM_GROUP(3);
@@ -918,39 +921,33 @@ void persistent_kernel(const half_t* __restrict__ A, const half_t* __restrict__ 
       if constexpr (kNext) FASTMM_STRIP_READ(kNextSlot, 1 - kSet);
       if constexpr (kLoad) strip_load(load_kt, kSlot);
     }
-    static_assert(kWait == 16 || kWait == 48, "steady (16) or tile-start (48) wait");
-    if constexpr (kWait == 16 && kWaitSteady == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-    else if constexpr (kWait == 16 && kWaitSteady == 18) asm volatile("s_waitcnt vmcnt(18)" ::: "memory");
-    else if constexpr (kWait == 48 && kWaitFirst == 48) asm volatile("s_waitcnt vmcnt(48)" ::: "memory");
-    else if constexpr (kWait == 48 && kWaitFirst == 51) asm volatile("s_waitcnt vmcnt(51)" ::: "memory");
-    else static_assert(kWait < 0, "unsupported vmcnt");
+    wait_loads();
     if constexpr (kNext) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     fast::barrier();
   };
-  // A tile's first four slices (refilled with its slices 4..7; the first two
-  // waits allow the previous tile's stores in flight).
+  // A tile's first four slices (refilled with its slices 4..7).
   auto first_group = [&]() __attribute__((always_inline)) {
-    step(4, Int<0>{}, Bool<true>{}, Bool<true>{}, Int<48>{}, Bool<true>{});
-    step(5, Int<1>{}, Bool<true>{}, Bool<true>{}, Int<48>{}, Bool<false>{});
-    step(6, Int<2>{}, Bool<true>{}, Bool<true>{}, Int<16>{}, Bool<false>{});
-    step(7, Int<3>{}, Bool<true>{}, Bool<true>{}, Int<16>{}, Bool<false>{});
+    step(4, Int<0>{}, Bool<true>{}, Bool<true>{}, Bool<true>{});
+    step(5, Int<1>{}, Bool<true>{}, Bool<true>{}, Bool<false>{});
+    step(6, Int<2>{}, Bool<true>{}, Bool<true>{}, Bool<false>{});
+    step(7, Int<3>{}, Bool<true>{}, Bool<true>{}, Bool<false>{});
     fence();
   };
   auto steady_group = [&](int load_kt) __attribute__((always_inline)) {
-    step(load_kt, Int<0>{}, Bool<true>{}, Bool<true>{}, Int<16>{}, Bool<false>{});
-    step(load_kt + 1, Int<1>{}, Bool<true>{}, Bool<true>{}, Int<16>{}, Bool<false>{});
-    step(load_kt + 2, Int<2>{}, Bool<true>{}, Bool<true>{}, Int<16>{}, Bool<false>{});
-    step(load_kt + 3, Int<3>{}, Bool<true>{}, Bool<true>{}, Int<16>{}, Bool<false>{});
+    step(load_kt, Int<0>{}, Bool<true>{}, Bool<true>{}, Bool<false>{});
+    step(load_kt + 1, Int<1>{}, Bool<true>{}, Bool<true>{}, Bool<false>{});
+    step(load_kt + 2, Int<2>{}, Bool<true>{}, Bool<true>{}, Bool<false>{});
+    step(load_kt + 3, Int<3>{}, Bool<true>{}, Bool<true>{}, Bool<false>{});
     fence();
   };
   // A tile's last four slices: the refills fetch slices 0..3 of the next tile
   // (the descriptor was switched), and the last step reads no fragments, so
   // both fragment sets are free in the epilogue.
   auto boundary_group = [&]() __attribute__((always_inline)) {
-    step(0, Int<0>{}, Bool<true>{}, Bool<true>{}, Int<16>{}, Bool<false>{});
-    step(1, Int<1>{}, Bool<true>{}, Bool<true>{}, Int<16>{}, Bool<false>{});
-    step(2, Int<2>{}, Bool<true>{}, Bool<true>{}, Int<16>{}, Bool<false>{});
-    step(3, Int<3>{}, Bool<true>{}, Bool<false>{}, Int<16>{}, Bool<false>{});
+    step(0, Int<0>{}, Bool<true>{}, Bool<true>{}, Bool<false>{});
+    step(1, Int<1>{}, Bool<true>{}, Bool<true>{}, Bool<false>{});
+    step(2, Int<2>{}, Bool<true>{}, Bool<true>{}, Bool<false>{});
+    step(3, Int<3>{}, Bool<true>{}, Bool<false>{}, Bool<false>{});
     fence();
   };
   // Slice-0 fragments (ring slot 0) into register set 0; every wave's reads
@@ -974,19 +971,7 @@ void persistent_kernel(const half_t* __restrict__ A, const half_t* __restrict__ 
     for (int idx = 0; idx < 8; ++idx) load_one(s, s, idx);
     if constexpr (kStrip) strip_load(s, s);
   }
-  {
-    // stores that write nothing (no records), in the place of a previous tile's
-    const __amdgpu_buffer_rsrc_t none = __builtin_amdgcn_make_buffer_rsrc(P, 0, 0, 0x00020000);
-    asm volatile("" ::: "memory");
-#pragma unroll
-    for (int q = 0; q < kStoresPerWave; ++q)
-      __builtin_amdgcn_raw_buffer_store_b128(uint4v{0, 0, 0, 0}, none, kOutOfRange, 0, 0);
-    asm volatile("" ::: "memory");
-  }
-  // slices 0 and 1 resident
-  if constexpr (kWaitFirst == 48) asm volatile("s_waitcnt vmcnt(48)" ::: "memory");
-  else if constexpr (kWaitFirst == 51) asm volatile("s_waitcnt vmcnt(51)" ::: "memory");
-  else static_assert(kWaitFirst < 0, "unsupported vmcnt");
+  wait_loads();  // slices 0 and 1 resident
   fast::barrier();
   set_strip(first);
   read_first_slice();

@@ -129,6 +129,42 @@ def test_main_loop_shape(assembly) -> None:
         assert shapes == {256}, (name, shapes)
 
 
+def _asm_vmcnt_waits(body: str) -> list[int]:
+    """The vmcnt bounds of the kernel's own waits: those written as inline asm
+    (between the ;;#ASMSTART / ;;#ASMEND markers), not the compiler's."""
+    return [int(n) for block in re.findall(r";;#ASMSTART(.*?);;#ASMEND", body, re.S)
+            for n in re.findall(r"s_waitcnt[^\n]*vmcnt\((\d+)\)", block)]
+
+
+def _persistent_wait_violations(assembly: str) -> list[str]:
+    """The persistent kernel's waits may leave only loads in flight: vmcnt also
+    counts stores, and a store can complete before older loads, so a bound that
+    allowed stores would not prove the awaited loads had landed. The kernel's own
+    waits (the prologue's and every step's) are two steps of loads (16; 18 with
+    the strip), the last one vmcnt(0), and no store precedes the first wait."""
+    found = []
+    for name, body in _kernels(assembly).items():
+        flags = re.search(r"persistent_kernelILi\dELi\dELb[01]ELb([01])E", name)
+        if not flags:
+            continue
+        loads = 18 if flags.group(1) == "1" else 16
+        waits = _asm_vmcnt_waits(body)
+        found += [f"{name}: vmcnt({n})" for n in waits[:-1] if n != loads]
+        if waits[-1:] != [0]:
+            found.append(f"{name}: the last wait is not vmcnt(0)")
+        if "buffer_store" in body[: body.index("vmcnt(")]:
+            found.append(f"{name}: a store before the first wait")
+    return found
+
+
+def test_persistent_waits_leave_only_loads_in_flight(assembly) -> None:
+    assert _persistent_wait_violations(assembly) == []
+    # a tile-start wait that lets the previous tile's stores stay in flight is caught
+    at = assembly.index("s_waitcnt vmcnt(16)", re.search(r"_ZN6fastmm6mfma1617persistent_kernel\w*:", assembly).end())
+    planted = assembly[:at] + "s_waitcnt vmcnt(48)" + assembly[at + len("s_waitcnt vmcnt(16)"):]
+    assert len(_persistent_wait_violations(planted)) == 1
+
+
 def test_thin_row_kernels_touch_no_load_in_flight(assembly) -> None:
     names = [m.group(1) for m in _build.ASM_LOAD_CHECKED_KERNELS.finditer(assembly)]
     for variant in ("ILi1ELi1E", "ILi1ELi2E", "ILi0ELi0E", "ILi0ELi2E"):
