@@ -111,7 +111,8 @@ def test_load_expanded_rank49_scheme() -> None:
     assert len(scheme.left_coefficients) == 49 and all(len(r) == 16 for r in scheme.left_coefficients)
     assert len(scheme.right_coefficients) == 49 and all(len(r) == 16 for r in scheme.right_coefficients)
     assert len(scheme.output_coefficients) == 16 and all(len(r) == 49 for r in scheme.output_coefficients)
-    # rank 49 is Strassen (x) Strassen: 14^2 nonzeros per factor (SURVEY scheme facts).
+    # rank 49 is the Kronecker square of the 2x2x2 rank-7 scheme, whose factor matrices
+    # hold 14 nonzeros each: 14^2 = 196 per factor matrix here.
     for matrix in (scheme.left_coefficients, scheme.right_coefficients, scheme.output_coefficients):
         assert sum(1 for row in matrix for value in row if value) == 196
         assert {value for row in matrix for value in row} <= {-1, 0, 1}
