@@ -334,6 +334,47 @@ def test_persistent_and_per_tile_kernels_agree_bitwise(rank, mb, kb, nb, scale, 
         assert ((together != 0) & (together.abs() < 2.0**-14)).any()
 
 
+def _persistent_random_shapes(count: int = 24) -> list[tuple[int, int, int, int]]:
+    """Seeded (rank, Mb, Kb, Nb): one leaf fits a round of 256x256 tiles on a 256-CU
+    device (the per-tile kernel), all of them need more (the persistent kernel)."""
+    rng = np.random.default_rng(4242)
+    shapes = []
+    while len(shapes) < count:
+        mb, nb = int(rng.integers(300, 3300)), int(rng.integers(40, 380)) * 8
+        kb = int(rng.choice([256, 384, 512, 768, 1024]))
+        per_leaf = -(-mb // 256) * -(-nb // 256)
+        if not 4 <= per_leaf <= 256:
+            continue
+        low = 256 // per_leaf + 1
+        rank = int(rng.integers(low, max(low + 1, 2200 // per_leaf)))
+        if 256 < rank * per_leaf <= 2200 and rank * mb * nb * 2 <= 1.5e9:
+            shapes.append((rank, mb, kb, nb))
+    return shapes
+
+
+@pytest.mark.parametrize(("rank", "mb", "kb", "nb"), _persistent_random_shapes())
+def test_persistent_kernel_matches_per_tile_on_random_shapes(rank, mb, kb, nb) -> None:
+    """Seeded random shapes, ragged rows and columns, every workgroup's first tile and
+    later ones: the persistent kernel's products (all leaves in one call) equal the
+    per-tile kernel's (one leaf per call) bit for bit, no scratch (no split-K tail)."""
+    print(f"\n[case] persistent vs per-tile, random {(rank, mb, kb, nb)}", flush=True)
+    cus = torch.cuda.get_device_properties(DEVICE).multi_processor_count
+    per_leaf = -(-mb // 256) * -(-nb // 256)
+    if not per_leaf <= cus < rank * per_leaf:
+        pytest.skip(f"{cus} compute units: the shape does not split into both paths")
+    g = torch.Generator(device=DEVICE).manual_seed(rank * mb + kb * nb)
+    a = torch.randn((rank, mb, kb), device=DEVICE, generator=g).to(torch.float16)
+    b = torch.randn((rank, nb, kb), device=DEVICE, generator=g).to(torch.float16)
+    together = torch.full((rank, mb, nb), float("nan"), device=DEVICE, dtype=torch.float16)
+    apart = torch.full((rank, mb, nb), float("nan"), device=DEVICE, dtype=torch.float16)
+    _stages.leaf_products(rank, a, b, together, mb, kb, nb)
+    for r in range(rank):
+        _stages.leaf_products(1, a[r : r + 1], b[r : r + 1], apart[r : r + 1], mb, kb, nb)
+    torch.cuda.synchronize()
+    assert not torch.isnan(together).any()
+    assert torch.equal(together.view(torch.int16), apart.view(torch.int16))
+
+
 @pytest.mark.parametrize(
     ("rank", "mb", "kb", "nb", "dtype", "product_dtype"),
     (
