@@ -26,7 +26,9 @@ star's rank-48 point at 8214 x 12288 x 4608) runs on its own seeded inputs
   stay below its rel-L2 5e-3 bound.
 
 C1 (1024^3, rank 7) is small enough to check against the oracle's whole
-evaluation.
+evaluation. The same checks run on open-model MLP down projections at row counts
+inside families of the shipped dispatch table (the shapes the Linear rewrite
+sends to the plans).
 """
 
 from __future__ import annotations
@@ -56,6 +58,14 @@ CONFIGS = {
     "C5-control-rank49-8192": ("rank49", 8192, 8192, 8192, False),
     "target-rank48-8214x12288x4608": ("rank48", 8214, 12288, 4608, False),
 }
+# open-model down projections (rows, K -> N) inside measured prepacked families
+MODEL_SHAPES = {
+    "Qwen2.5-32B-down-8192-rank7": ("rank7", 8192, 27648, 5120, False),
+    "Qwen2.5-32B-down-8192-rank48": ("rank48", 8192, 27648, 5120, False),
+    "Mistral-Nemo-12B-down-5000-rank7": ("rank7", 5000, 14336, 5120, False),
+    "Gemma-2-9B-down-7500-rank48": ("rank48", 7500, 14336, 3584, False),
+    "Qwen2.5-7B-down-12000-rank7": ("rank7", 12000, 18944, 3584, False),
+}
 # Rank 49's fp16 planes alone cost ~1.4x native BF16's error (the oracle's
 # prediction; measured 1.67x with fp16 products), beyond the 1.2x bound.
 RANK49_BAND = (1.2, 1.9)
@@ -84,9 +94,9 @@ def macroblock_tile_errors(plan, x, w, b, output) -> list[float]:
     return errors
 
 
-@pytest.mark.parametrize("config", list(CONFIGS))
+@pytest.mark.parametrize("config", list(CONFIGS) + list(MODEL_SHAPES))
 def test_baseline_config_through_the_hip_path(config: str) -> None:
-    key, m, k, n, has_bias = CONFIGS[config]
+    key, m, k, n, has_bias = {**CONFIGS, **MODEL_SHAPES}[config]
     print(f"\n[case] {config}: {key} {m}x{k}x{n} bias={has_bias}", flush=True)
     torch.cuda.empty_cache()
     rng = np.random.default_rng(zlib.crc32(config.encode()))
