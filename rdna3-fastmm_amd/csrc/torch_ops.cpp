@@ -50,7 +50,8 @@ void* stream_of(const at::Tensor& tensor) {
   return c10::hip::getCurrentHIPStream(tensor.device().index()).stream();
 }
 
-int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+// ceil(a / b) for b > 0; 0 for a <= 0
+int64_t ceil_div(int64_t a, int64_t b) { return a > 0 ? (a - 1) / b + 1 : 0; }
 
 // Buffer shape of a transformed operand (rows = Mb or Nb): K-slab-major
 // [R, Kb/32, rows, 32] when Kb % 32 == 0, else row-major [R, rows, Kb].
@@ -60,9 +61,55 @@ std::vector<int64_t> operand_shape(int64_t rank, int64_t rows, int64_t inner) {
 }
 
 // ---------------------------------------------------------------- stage ops
+//
+// The library sees bare pointers, so each stage operator first checks every
+// tensor against the dimensions it is given: on the first operand's ROCm
+// device, contiguous, and holding at least the elements the launch reads or
+// writes. A dimension that is not positive skips the count and reaches the
+// library, which rejects it before any launch.
+
+// Elements a launch over these extents covers (0 when one is not positive).
+int64_t covered(const char* op, std::initializer_list<int64_t> extents) {
+  for (int64_t e : extents)
+    if (e < 1) return 0;
+  int64_t n = 1;
+  for (int64_t e : extents)
+    TORCH_CHECK_VALUE(!__builtin_mul_overflow(n, e, &n), op, ": dimensions too large");
+  return n;
+}
+
+void require_buffer(const char* op, const char* name, const at::Tensor& tensor, const at::Device& device,
+                    int64_t elements) {
+  TORCH_CHECK_VALUE(tensor.device().is_cuda() && tensor.device() == device, op, ": ", name,
+                    " must be on the operands' ROCm device (", device, "), got ", tensor.device());
+  TORCH_CHECK_VALUE(tensor.is_contiguous(), op, ": ", name, " must be contiguous");
+  TORCH_CHECK_VALUE(tensor.numel() >= elements, op, ": ", name, " holds ", tensor.numel(),
+                    " elements, the launch covers ", elements);
+}
+
+struct SchemeDims {
+  int64_t size, rank;
+};
+
+SchemeDims scheme_dims(int64_t scheme) {
+  int s = 0, rank = 0;
+  check_status(fastmm_scheme_info(static_cast<int>(scheme), &s, &rank), "fastmm_scheme_info");
+  return {s, rank};
+}
+
+// Source [rows, inner] (or [inner, columns]) and planes [R, ceil(a/s), ceil(b/s)].
+void check_transform(const char* op, int64_t scheme, const at::Tensor& source, const at::Tensor& planes,
+                     int64_t a, int64_t b) {
+  TORCH_CHECK_VALUE(source.device().is_cuda(), op, ": tensors must be on a ROCm device, got ", source.device());
+  const SchemeDims d = scheme_dims(scheme);
+  require_buffer(op, "source", source, source.device(), covered(op, {a, b}));
+  require_buffer(op, "planes", planes, source.device(),
+                 covered(op, {d.rank, ceil_div(a, d.size), ceil_div(b, d.size)}));
+}
 
 void left_transform(int64_t scheme, const at::Tensor& input, const at::Tensor& output, int64_t rows,
                     int64_t inner) {
+  check_transform("rdna3_fastmm_hip::left_transform", scheme, input, output, rows, inner);
   c10::DeviceGuard guard(input.device());
   check_status(fastmm_left_transform(static_cast<int>(scheme), dtype_code(input.scalar_type()),
                                      dtype_code(output.scalar_type()), input.data_ptr(), output.data_ptr(), rows,
@@ -72,6 +119,7 @@ void left_transform(int64_t scheme, const at::Tensor& input, const at::Tensor& o
 
 void weight_transform(int64_t scheme, const at::Tensor& weight, const at::Tensor& output, int64_t columns,
                       int64_t inner) {
+  check_transform("rdna3_fastmm_hip::weight_transform", scheme, weight, output, columns, inner);
   c10::DeviceGuard guard(weight.device());
   check_status(fastmm_weight_transform(static_cast<int>(scheme), dtype_code(weight.scalar_type()),
                                        dtype_code(output.scalar_type()), weight.data_ptr(), output.data_ptr(),
@@ -81,6 +129,7 @@ void weight_transform(int64_t scheme, const at::Tensor& weight, const at::Tensor
 
 void right_transform(int64_t scheme, const at::Tensor& right, const at::Tensor& output, int64_t inner,
                      int64_t columns) {
+  check_transform("rdna3_fastmm_hip::right_transform", scheme, right, output, inner, columns);
   c10::DeviceGuard guard(right.device());
   check_status(fastmm_right_transform(static_cast<int>(scheme), dtype_code(right.scalar_type()),
                                       dtype_code(output.scalar_type()), right.data_ptr(), output.data_ptr(), inner,
@@ -91,6 +140,13 @@ void right_transform(int64_t scheme, const at::Tensor& right, const at::Tensor& 
 void leaf_products(int64_t rank, const at::Tensor& left, const at::Tensor& right, const at::Tensor& products,
                    int64_t block_rows, int64_t block_inner, int64_t block_columns,
                    const std::optional<at::Tensor>& scratch) {
+  const char* op = "rdna3_fastmm_hip::leaf_products";
+  TORCH_CHECK_VALUE(left.device().is_cuda(), op, ": tensors must be on a ROCm device, got ", left.device());
+  TORCH_CHECK_VALUE(right.scalar_type() == left.scalar_type(), op, ": left and right planes differ in dtype");
+  require_buffer(op, "left planes", left, left.device(), covered(op, {rank, block_rows, block_inner}));
+  require_buffer(op, "right planes", right, left.device(), covered(op, {rank, block_columns, block_inner}));
+  require_buffer(op, "products", products, left.device(), covered(op, {rank, block_rows, block_columns}));
+  if (scratch.has_value()) require_buffer(op, "scratch", *scratch, left.device(), 0);
   c10::DeviceGuard guard(left.device());
   void* scratch_data = scratch.has_value() ? scratch->data_ptr() : nullptr;
   const int64_t scratch_bytes = scratch.has_value() ? scratch->numel() * scratch->element_size() : 0;
@@ -113,6 +169,16 @@ int64_t leaf_scratch_bytes(int64_t rank, at::ScalarType operand_type, at::Scalar
 
 void reconstruct(int64_t scheme, const at::Tensor& products, const std::optional<at::Tensor>& bias,
                  const at::Tensor& output, int64_t rows, int64_t columns) {
+  const char* op = "rdna3_fastmm_hip::reconstruct";
+  TORCH_CHECK_VALUE(products.device().is_cuda(), op, ": tensors must be on a ROCm device, got ", products.device());
+  const SchemeDims d = scheme_dims(scheme);
+  require_buffer(op, "products", products, products.device(),
+                 covered(op, {d.rank, ceil_div(rows, d.size), ceil_div(columns, d.size)}));
+  require_buffer(op, "output", output, products.device(), covered(op, {rows, columns}));
+  if (bias.has_value()) {
+    TORCH_CHECK_VALUE(bias->scalar_type() == output.scalar_type(), op, ": bias must have the output's dtype");
+    require_buffer(op, "bias", *bias, products.device(), covered(op, {columns}));
+  }
   c10::DeviceGuard guard(products.device());
   check_status(fastmm_reconstruct(static_cast<int>(scheme), dtype_code(products.scalar_type()), products.data_ptr(),
                                   bias.has_value() ? bias->data_ptr() : nullptr, dtype_code(output.scalar_type()),

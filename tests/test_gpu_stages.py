@@ -425,3 +425,53 @@ def test_thin_tile_row_matches_full_tiles_bitwise(rank, mb, kb, nb, dtype, produ
     assert not torch.isnan(thin).any()
     bits = torch.int32 if product_dtype == torch.float32 else torch.int16
     assert torch.equal(thin.view(bits), full[:, :mb].contiguous().view(bits))
+
+
+def test_stage_operators_check_buffers_before_any_launch() -> None:
+    """Undersized, non-contiguous, mistyped or host buffers raise ValueError in the
+    operators before the C ABI sees a pointer: the sentinels in every buffer survive,
+    and the same calls with whole buffers go through."""
+    print("\n[case] stage operator buffer checks", flush=True)
+    scheme = load_scheme("rank7")
+    m, k, n = 64, 96, 80
+    s, r = scheme.size, scheme.rank
+    mb, kb, nb = m // s, k // s, n // s
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn((m, k), generator=g).to(torch.float16).to(DEVICE)
+    w = torch.randn((n, k), generator=g).to(torch.float16).to(DEVICE)
+    bias = torch.zeros((n,), device=DEVICE, dtype=torch.float16)
+    a = torch.full((r * mb * kb,), 7.0, device=DEVICE, dtype=torch.float16)
+    b = torch.full((r * nb * kb,), 7.0, device=DEVICE, dtype=torch.float16)
+    p = torch.full((r * mb * nb,), 7.0, device=DEVICE, dtype=torch.float16)
+    out = torch.full((m, n), 7.0, device=DEVICE, dtype=torch.float16)
+    right = w.t().contiguous()
+    cases = (
+        (lambda: _stages.left_transform(scheme, x, a[:-1], m, k), "planes holds"),
+        (lambda: _stages.left_transform(scheme, x.t(), a, k, m), "source must be contiguous"),
+        (lambda: _stages.left_transform(scheme, x, a.cpu(), m, k), "planes must be on the operands' ROCm device"),
+        (lambda: _stages.weight_transform(scheme, w, b[:-1], n, k), "planes holds"),
+        (lambda: _stages.right_transform(scheme, right[:-1], b, k, n), "source holds"),
+        (lambda: _stages.leaf_products(r, a, b, p[:-1], mb, kb, nb), "products holds"),
+        (lambda: _stages.leaf_products(r, a, b[:-1], p, mb, kb, nb), "right planes holds"),
+        (lambda: _stages.leaf_products(r, a, b.bfloat16(), p, mb, kb, nb), "differ in dtype"),
+        (lambda: _stages.leaf_products(r, a, b, p, mb, kb, nb, torch.zeros(64, dtype=torch.uint8)),
+         "scratch must be on"),
+        (lambda: _stages.reconstruct(scheme, p, None, out[:-1], m, n), "output holds"),
+        (lambda: _stages.reconstruct(scheme, p[:-1], None, out, m, n), "products holds"),
+        (lambda: _stages.reconstruct(scheme, p, bias[:-1], out, m, n), "bias holds"),
+        (lambda: _stages.reconstruct(scheme, p, bias.float(), out, m, n), "bias must have the output's dtype"),
+        (lambda: _stages.reconstruct(scheme, p.cpu(), None, out, m, n), "must be on a ROCm device"),
+    )
+    for call, message in cases:
+        with pytest.raises(ValueError, match=message):
+            call()
+    torch.cuda.synchronize()
+    for buffer in (a, b, p, out):
+        assert bool((buffer == 7.0).all())
+    _stages.left_transform(scheme, x, a, m, k)
+    _stages.weight_transform(scheme, w, b, n, k)
+    _stages.leaf_products(r, a, b, p, mb, kb, nb)
+    _stages.reconstruct(scheme, p, bias, out, m, n)
+    torch.cuda.synchronize()
+    expected = x.float() @ w.float().t()
+    assert torch.allclose(out.float(), expected, rtol=2e-2, atol=0.5)

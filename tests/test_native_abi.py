@@ -145,3 +145,26 @@ def test_torch_operators_reject_bad_operands_before_any_launch(shapes, dtypes, m
     for op in (_torch_ops.linear, _torch_ops.linear_rank7, _torch_ops.linear_rank48):
         with pytest.raises(ValueError, match=message):
             op(x, w)
+
+
+def test_stage_operators_reject_host_tensors_before_any_launch() -> None:
+    """Every stage operator checks its tensors before the C ABI sees a pointer:
+    host tensors are refused with a ValueError (no launch, no library status)."""
+    import torch
+
+    from rdna3_fastmm import _torch_ops
+
+    stages = _torch_ops.stages
+    scheme = load_scheme("rank7").scheme_id
+    x = torch.zeros((4, 4), dtype=torch.float16)
+    planes = torch.zeros((7, 2, 2), dtype=torch.float16)
+    calls = (
+        lambda: stages.left_transform(scheme, x, planes, 4, 4),
+        lambda: stages.weight_transform(scheme, x, planes, 4, 4),
+        lambda: stages.right_transform(scheme, x, planes, 4, 4),
+        lambda: stages.leaf_products(7, planes, planes, planes.clone(), 2, 2, 2, None),
+        lambda: stages.reconstruct(scheme, planes, None, x, 4, 4),
+    )
+    for call in calls:
+        with pytest.raises(ValueError, match="must be on a ROCm device"):
+            call()
