@@ -149,8 +149,8 @@ def _linear_node_target(node: Node) -> Optional[Callable]:
     columns, weight_inner = weight.shape
     if inner != weight_inner:
         return None
-    if not all(isinstance(d, int) for d in (*input_tensor.shape[:-1], inner, columns)):
-        return None
+    if not all(isinstance(d, int) and d > 0 for d in (*input_tensor.shape[:-1], inner, columns)):
+        return None  # symbolic or empty: left to aten
     has_bias = bias_node is not None
     if isinstance(bias_node, Node):
         bias = _node_tensor(bias_node)

@@ -82,6 +82,8 @@ def test_rewrite_flattens_leading_dimensions(measured) -> None:
         (((3072, 4608), (12288, 4608)), torch.bfloat16, "cuda"),  # rows outside the family
         (((5120, 4608), (12288, 4608)), torch.float16, "cuda"),  # not BF16
         (((5120, 4608), (12288, 4608)), torch.bfloat16, "cpu"),  # not on the GPU
+        (((5120, 0), (12288, 0)), torch.bfloat16, "cuda"),  # empty inner dimension
+        (((0, 4608), (12288, 4608)), torch.bfloat16, "cuda"),  # no rows
     ),
 )
 def test_rewrite_preserves_ineligible_linear(measured, shapes, dtype, device) -> None:
