@@ -65,6 +65,8 @@ MODEL_SHAPES = {
     "Mistral-Nemo-12B-down-5000-rank7": ("rank7", 5000, 14336, 5120, False),
     "Gemma-2-9B-down-7500-rank48": ("rank48", 7500, 14336, 3584, False),
     "Qwen2.5-7B-down-12000-rank7": ("rank7", 12000, 18944, 3584, False),
+    "Qwen3-32B-down-6000-rank48": ("rank48", 6000, 25600, 5120, False),
+    "Yi-34B-down-4100-rank7": ("rank7", 4100, 20480, 7168, False),  # Mb = 2050: a 2-row strip
 }
 # Rank 49's fp16 planes alone cost ~1.4x native BF16's error (the oracle's
 # prediction; measured 1.67x with fp16 products), beyond the 1.2x bound.

@@ -232,6 +232,11 @@ def test_shipped_dispatch_table_is_consistent() -> None:
         assert Rank7Plan.has_measured_linear_win((8214, 12288, 4608), has_bias=bias)
         assert Rank48Plan.has_measured_linear_win((8214, 12288, 4608), has_bias=bias, prepacked_weight=True)
     assert not Rank7Plan.has_measured_linear_win((8192, 12288, 4608), has_bias=False, prepacked_weight=True)
+    # down projections of Qwen3-32B, Gemma-2-27B and Yi-34B inside swept families
+    assert Rank7Plan.has_measured_linear_win((8192, 25600, 5120), has_bias=False, prepacked_weight=True)
+    assert Rank48Plan.has_measured_linear_win((10240, 25600, 5120), has_bias=False, prepacked_weight=True)
+    assert Rank7Plan.has_measured_linear_win((12288, 36864, 4608), has_bias=False, prepacked_weight=True)
+    assert Rank48Plan.has_measured_linear_win((5120, 20480, 7168), has_bias=False, prepacked_weight=True)
 
 
 @pytest.mark.parametrize(
