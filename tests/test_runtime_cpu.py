@@ -237,6 +237,10 @@ def test_shipped_dispatch_table_is_consistent() -> None:
     assert Rank48Plan.has_measured_linear_win((10240, 25600, 5120), has_bias=False, prepacked_weight=True)
     assert Rank7Plan.has_measured_linear_win((12288, 36864, 4608), has_bias=False, prepacked_weight=True)
     assert Rank48Plan.has_measured_linear_win((5120, 20480, 7168), has_bias=False, prepacked_weight=True)
+    # and of DeepSeek-V3's dense layers, Mixtral-8x22B and Gemma-3-12B
+    assert Rank48Plan.has_measured_linear_win((5120, 18432, 7168), has_bias=False, prepacked_weight=True)
+    assert Rank48Plan.has_measured_linear_win((7168, 16384, 6144), has_bias=False, prepacked_weight=True)
+    assert Rank7Plan.has_measured_linear_win((10240, 15360, 3840), has_bias=False, prepacked_weight=True)
 
 
 @pytest.mark.parametrize(
