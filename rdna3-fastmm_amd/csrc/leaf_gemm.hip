@@ -741,10 +741,25 @@ void persistent_kernel(const half_t* __restrict__ A, const half_t* __restrict__ 
   __amdgpu_buffer_rsrc_t a_rsrc, b_rsrc;
   unsigned a_off[SEGMENTS], b_off[SEGMENTS];
   unsigned r_off = kOutOfRange;  // the strip's A' fragment (kStrip)
+  // Fragment-read redirect for the descriptor's tile (bytes, uniform). A wave
+  // whose 128 x 128 quadrant lies wholly past the leaf stores nothing, yet its
+  // MFMAs would multiply real rows by zero-filled ones at nearly the power of
+  // real work, and the leaf GEMM runs at the board's power limit. Such a wave
+  // reads both operands from its zero-filled quadrant instead (A' fragments
+  // from the zero B' rows past Nb, or B' fragments from the zero A' rows past
+  // Mb), so its MFMAs multiply zeros: the same instructions, waits and
+  // barriers, far less power. The other waves' products are unchanged.
+  int load_da = 0, load_db = 0;
   auto set_loads = [&](int logical) __attribute__((always_inline)) {
     const bool none = logical < 0;
     int leaf, tm, tn;
     tile_of(none ? 0 : logical, tiles_m, tiles_n, 8, leaf, tm, tn);
+    {
+      const int a_quadrant = wm * 128 * BK, b_quadrant = kTile * BK + wn * 128 * BK;  // halves into a slot
+      const bool past_columns = tn * kTile + wn * 128 >= Nb, past_rows = tm * kTile + wm * 128 >= Mb;
+      load_da = __builtin_amdgcn_readfirstlane(past_columns ? 2 * (b_quadrant - a_quadrant) : 0);
+      load_db = __builtin_amdgcn_readfirstlane(!past_columns && past_rows ? 2 * (a_quadrant - b_quadrant) : 0);
+    }
     a_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(A + static_cast<int64_t>(leaf) * Mb * Kb), 0,
                                                Mb * Kb * 2, 0x00020000);
     b_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(B + static_cast<int64_t>(leaf) * Nb * Kb), 0,
@@ -777,6 +792,18 @@ void persistent_kernel(const half_t* __restrict__ A, const half_t* __restrict__ 
     base_a[h] = (unsigned)(uintptr_t)(lds_ptr)(smem + h * 2 * STAGE_HALVES + wm * 128 * BK + rd);
     base_b[h] = (unsigned)(uintptr_t)(lds_ptr)(smem + h * 2 * STAGE_HALVES + kTile * BK + wn * 128 * BK + rd);
   }
+  // Moves the fragment bases to the descriptor's tile's redirect: called right
+  // before a tile's first fragment reads, after the previous tile's last ones.
+  int applied_da = 0, applied_db = 0;
+  auto redirect_reads = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      base_a[h] += static_cast<unsigned>(load_da - applied_da);
+      base_b[h] += static_cast<unsigned>(load_db - applied_db);
+    }
+    applied_da = load_da;
+    applied_db = load_db;
+  };
 
   half8 fa[2][FM], fb[2][FN];
   float4v acc[FM][FN];  // never zeroed: a tile's first MFMAs take srcC = 0
@@ -974,6 +1001,7 @@ void persistent_kernel(const half_t* __restrict__ A, const half_t* __restrict__ 
   wait_loads();  // slices 0 and 1 resident
   fast::barrier();
   set_strip(first);
+  redirect_reads();
   read_first_slice();
 
   for (int t = 0; t < count; ++t) {
@@ -1058,6 +1086,7 @@ void persistent_kernel(const half_t* __restrict__ A, const half_t* __restrict__ 
       asm volatile("" ::: "memory");
       if (t + 1 < count) set_strip(logical + stride);
     }
+    redirect_reads();  // the descriptor now holds the next tile
     read_first_slice();
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last (empty) refills have landed in LDS
