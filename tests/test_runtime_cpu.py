@@ -241,6 +241,9 @@ def test_shipped_dispatch_table_is_consistent() -> None:
     assert Rank48Plan.has_measured_linear_win((5120, 18432, 7168), has_bias=False, prepacked_weight=True)
     assert Rank48Plan.has_measured_linear_win((7168, 16384, 6144), has_bias=False, prepacked_weight=True)
     assert Rank7Plan.has_measured_linear_win((10240, 15360, 3840), has_bias=False, prepacked_weight=True)
+    # and of Mistral-Large-2 and Command-R+ (N = 12288)
+    assert Rank48Plan.has_measured_linear_win((8192, 28672, 12288), has_bias=False, prepacked_weight=True)
+    assert Rank48Plan.has_measured_linear_win((16384, 33792, 12288), has_bias=False, prepacked_weight=True)
 
 
 @pytest.mark.parametrize(
