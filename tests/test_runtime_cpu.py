@@ -244,6 +244,9 @@ def test_shipped_dispatch_table_is_consistent() -> None:
     # and of Mistral-Large-2 and Command-R+ (N = 12288)
     assert Rank48Plan.has_measured_linear_win((8192, 28672, 12288), has_bias=False, prepacked_weight=True)
     assert Rank48Plan.has_measured_linear_win((16384, 33792, 12288), has_bias=False, prepacked_weight=True)
+    # square attention output projections, in the few row ranges where native is slow
+    assert Rank48Plan.has_measured_linear_win((3072, 12288, 12288), has_bias=False, prepacked_weight=True)
+    assert Rank48Plan.has_measured_linear_win((4864, 8192, 8192), has_bias=False, prepacked_weight=True)
 
 
 @pytest.mark.parametrize(
