@@ -247,6 +247,9 @@ def test_shipped_dispatch_table_is_consistent() -> None:
     # square attention output projections, in the few row ranges where native is slow
     assert Rank48Plan.has_measured_linear_win((3072, 12288, 12288), has_bias=False, prepacked_weight=True)
     assert Rank48Plan.has_measured_linear_win((4864, 8192, 8192), has_bias=False, prepacked_weight=True)
+    # the output projection of Flux's single-stream blocks (attention and MLP halves together)
+    assert Rank7Plan.has_measured_linear_win((13312, 15360, 3072), has_bias=True, prepacked_weight=True)
+    assert not Rank7Plan.has_measured_linear_win((13312, 15360, 3072), has_bias=False, prepacked_weight=True)
 
 
 @pytest.mark.parametrize(
