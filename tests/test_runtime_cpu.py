@@ -250,6 +250,9 @@ def test_shipped_dispatch_table_is_consistent() -> None:
     # the output projection of Flux's single-stream blocks (attention and MLP halves together)
     assert Rank7Plan.has_measured_linear_win((13312, 15360, 3072), has_bias=True, prepacked_weight=True)
     assert not Rank7Plan.has_measured_linear_win((13312, 15360, 3072), has_bias=False, prepacked_weight=True)
+    # and of Mistral-Small-3 and Gemma-3-4B
+    assert Rank48Plan.has_measured_linear_win((8192, 32768, 5120), has_bias=False, prepacked_weight=True)
+    assert Rank7Plan.has_measured_linear_win((15360, 10240, 2560), has_bias=False, prepacked_weight=True)
 
 
 @pytest.mark.parametrize(
