@@ -254,6 +254,7 @@ def test_shipped_dispatch_table_is_consistent() -> None:
     assert Rank48Plan.has_measured_linear_win((8192, 32768, 5120), has_bias=False, prepacked_weight=True)
     assert Rank7Plan.has_measured_linear_win((15360, 10240, 2560), has_bias=False, prepacked_weight=True)
     assert Rank7Plan.has_measured_linear_win((12800, 11008, 2048), has_bias=False, prepacked_weight=True)  # Qwen2.5-3B
+    assert Rank7Plan.has_measured_linear_win((17024, 8192, 2048), has_bias=False, prepacked_weight=True)  # Llama-3.2-1B
 
 
 @pytest.mark.parametrize(
