@@ -647,11 +647,13 @@ void leaf_gemm_kernel(const half_t* __restrict__ A, const half_t* __restrict__ B
 // range decode_tile gives), gridDim.x / 8 tiles apart. One continuous slice
 // stream: in a tile's last four slices the refills already fetch the next
 // tile's first four, so a tile starts without waiting for memory. The output
-// leaves through a 32 KB staging area after the 128 KB ring, in four chunks of
-// 64 rows (32 from each half of the tile, so every wave writes every chunk;
-// 16-byte chunks XOR-swizzled by row: conflict-free 8-byte writes), as full
-// 512-byte row segments (rows or columns past the leaf get an out-of-range
-// offset and write nothing). Every wait leaves at most two steps of loads in
+// leaves through a 32 KB staging area after the 128 KB ring: each wave stages
+// its own 128 x 128 quadrant through a private 8 KB slice (16-byte chunks
+// XOR-swizzled by row: conflict-free 8-byte writes), 32 rows at a time, and
+// stores 4 rows x 256 bytes per instruction (rows or columns past the leaf get
+// an out-of-range offset and write nothing). A wave whose quadrant lies wholly
+// past the leaf reads zeros for both MFMA operands (see set_loads), so its
+// unstored products cost little power. Every wait leaves at most two steps of loads in
 // flight and nothing else: vmcnt counts stores as well, and a store can
 // complete before older loads (one past the buffer completes at once), so a
 // wait that allowed a tile's stores in flight would not prove that the loads
