@@ -16,7 +16,7 @@ so Dynamo/Inductor treat them as opaque extern kernels.
 graph before AOT compilation, exactly where the reference does
 (linear.py:170-288): BF16 input/weight/bias on one GPU, contiguous, static
 shape, a measured-win family, and at most half of the free device memory
-for the temporaries. The reference tries rank-7 families first, then rank-49
+for the temporaries (here also the split-K scratch). The reference tries rank-7 families first, then rank-49
 (linear.py:240-252); here every scheme with measured MI355X families is a
 candidate (rank 7, rank 48, rank 49) and the one whose covering family was
 measured fastest is used, earlier schemes winning ties.
@@ -33,6 +33,9 @@ from .runtime import Rank7Plan, Rank48Plan, Rank49Plan, _LinearPlan
 
 LINEAR_TARGETS = frozenset({torch._C._nn.linear, torch.ops.aten.linear.default})
 MAX_LINEAR_ALLOCATION_FREE_FRACTION = 0.5
+# The most split-K scratch one call allocates: 192 fp32 256 x 256 tile parts, the
+# tail planner's maximum on a 256-CU MI355X (FASTMM_STATIC_SCRATCH_BYTES).
+MAX_LEAF_SCRATCH_BYTES = 48 << 20
 
 
 def _ceil_div(a: int, b: int) -> int:
@@ -95,11 +98,13 @@ def _node_tensor(node: Node) -> Optional[torch.Tensor]:
 
 
 def _has_linear_memory_budget(plan_type: type, shape: tuple, device: torch.device) -> bool:
-    """Temporaries of one dynamic call fit in half the free memory (linear.py:175-194)."""
+    """Temporaries of one dynamic call fit in half the free memory (linear.py:175-194):
+    the reference's planes, products and output, plus this backend's split-K scratch
+    (counted at its maximum; the operator may allocate less)."""
     rows, inner, columns = shape
     s, rank = plan_type.scheme_size, plan_type.rank
     mb, kb, nb = _ceil_div(rows, s), _ceil_div(inner, s), _ceil_div(columns, s)
-    allocation = rank * (mb * kb + kb * nb + mb * nb) * 2 + rows * columns * 2
+    allocation = rank * (mb * kb + kb * nb + mb * nb) * 2 + rows * columns * 2 + MAX_LEAF_SCRATCH_BYTES
     free_bytes, _ = torch.cuda.mem_get_info(device)
     return allocation <= free_bytes * MAX_LINEAR_ALLOCATION_FREE_FRACTION
 

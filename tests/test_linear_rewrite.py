@@ -99,6 +99,19 @@ def test_rewrite_preserves_linear_without_memory_budget(measured, monkeypatch) -
     assert rewrite_eligible_linears(gm, [x, w]) == 0
 
 
+def test_memory_budget_counts_the_split_k_scratch(measured, monkeypatch) -> None:
+    """Planes, products and output (the reference's sum) plus the leaf GEMM's split-K
+    scratch at its 48 MiB maximum must fit in half the free memory."""
+    rows, inner, columns = 5120, 4608, 12288
+    mb, kb, nb = rows // 2, inner // 2, columns // 2
+    temporaries = 7 * (mb * kb + kb * nb + mb * nb) * 2 + rows * columns * 2
+    for free, expected in ((2 * temporaries, 0), (2 * (temporaries + (48 << 20)), 1)):
+        monkeypatch.setattr(torch.cuda, "mem_get_info", lambda device=None, free=free: (free, 288 << 30))
+        (x, w), _ = fake((rows, inner), (columns, inner))
+        gm = traced(Linear(), x, w)
+        assert rewrite_eligible_linears(gm, [x, w]) == expected, free
+
+
 def test_rewrite_rejects_non_contiguous_weight(measured) -> None:
     (x, w), mode = fake((5120, 4608), (4608, 12288))
     with mode:
