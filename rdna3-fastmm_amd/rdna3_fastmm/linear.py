@@ -16,10 +16,11 @@ so Dynamo/Inductor treat them as opaque extern kernels.
 graph before AOT compilation, exactly where the reference does
 (linear.py:170-288): BF16 input/weight/bias on one GPU, contiguous, static
 shape, a measured-win family, and at most half of the free device memory
-for the temporaries (here also the split-K scratch). The reference tries rank-7 families first, then rank-49
-(linear.py:240-252); here every scheme with measured MI355X families is a
-candidate (rank 7, rank 48, rank 49) and the one whose covering family was
-measured fastest is used, earlier schemes winning ties.
+for the temporaries (here also the split-K scratch). The reference tries
+rank-7 families first, then rank-49 (linear.py:240-252); here every scheme
+with measured MI355X families is a candidate (rank 7, rank 48, rank 49) and
+the one whose covering family was measured fastest is used, earlier schemes
+winning ties.
 """
 
 from typing import Callable, Optional
