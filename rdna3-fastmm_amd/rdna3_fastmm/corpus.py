@@ -414,12 +414,13 @@ def row_intervals(points: list[tuple[int, float, float]], minimum_speedup: float
     return runs
 
 
-def sweep_families(reports: list[dict], minimum_speedup: float) -> list[dict]:
+def sweep_families(reports: list[dict], minimum_speedup: float, minimum_runs: int = 1) -> list[dict]:
     """Row-interval families per (scheme, mode, inner, columns, bias) of a sweep.
 
     Reports of repeated sweeps (other boxes, other days) combine point by
     point: a row counts with its slowest speedup and worst error ratio, so a
-    family is a run of rows that beat native in every measurement."""
+    family is a run of rows that beat native in every measurement. A row
+    measured fewer than ``minimum_runs`` times counts as no win."""
     measured: dict[tuple, dict[int, list[tuple[float, float]]]] = {}
     for report in reports:
         rows, inner, columns = report["case"]["shape"]
@@ -433,7 +434,8 @@ def sweep_families(reports: list[dict], minimum_speedup: float) -> list[dict]:
                     (entry["speedup_vs_native"], entry["error_ratio"]))
     families = []
     for (scheme, prepacked, inner, columns, bias), by_rows in sorted(measured.items()):
-        points = [(rows, min(s for s, _ in runs), max(r for _, r in runs)) for rows, runs in by_rows.items()]
+        points = [(rows, min(s for s, _ in runs) if len(runs) >= minimum_runs else 0.0, max(r for _, r in runs))
+                  for rows, runs in by_rows.items()]
         for low, high in row_intervals(points, minimum_speedup):
             inside = [speedup for rows, speedup, _ in points if low <= rows <= high]
             runs = min(len(runs) for rows, runs in by_rows.items() if low <= rows <= high)
@@ -446,7 +448,8 @@ def sweep_families(reports: list[dict], minimum_speedup: float) -> list[dict]:
 DISPATCH_SCHEMA_VERSION = 1
 
 
-def dispatch_document(reports: list[dict], minimum_speedup: float, measurement: str) -> dict:
+def dispatch_document(reports: list[dict], minimum_speedup: float, measurement: str,
+                      minimum_runs: int = 1) -> dict:
     """The runtime's dispatch table (``rdna3_fastmm/dispatch/mi355x.json``) from sweep reports."""
     devices = sorted({report.get("device", "?") for report in reports})
     torch_versions = sorted({report.get("torch", "?") for report in reports})
@@ -459,7 +462,7 @@ def dispatch_document(reports: list[dict], minimum_speedup: float, measurement: 
         "minimum_speedup": minimum_speedup,
         "error_ratio_bound": ERROR_RATIO_BOUND,
         "measurement": measurement,
-        "families": sweep_families(reports, minimum_speedup),
+        "families": sweep_families(reports, minimum_speedup, minimum_runs),
     }
 
 
@@ -506,6 +509,8 @@ def _arguments(argv: list[str] | None) -> argparse.Namespace:
     parser.add_argument("--rounds", type=int, default=9)
     parser.add_argument("--seed", type=int, default=0)
     parser.add_argument("--minimum-speedup", type=float, default=1.0)
+    parser.add_argument("--minimum-runs", type=int, default=1,
+                        help="with --summarize: rows measured fewer times than this never win")
     arguments = parser.parse_args(argv)
     running = arguments.case is not None or arguments.all or arguments.sweep is not None
     if running and arguments.output_directory is None:
@@ -522,13 +527,14 @@ def main(argv: list[str] | None = None) -> int:
     if arguments.summarize is not None:
         reports = [json.loads(p.read_text()) for d in arguments.summarize for p in sorted(d.glob("*.json"))]
         if arguments.dispatch_output is not None:
-            document = dispatch_document(reports, arguments.minimum_speedup, arguments.measurement)
+            document = dispatch_document(reports, arguments.minimum_speedup, arguments.measurement,
+                                         arguments.minimum_runs)
             arguments.dispatch_output.write_text(json.dumps(document, indent=1) + "\n")
             print(f"{len(document['families'])} families -> {arguments.dispatch_output}")
             return 0
         print(summary_table(reports))
         print(json.dumps(winning_families(reports, arguments.minimum_speedup), indent=1))
-        print(json.dumps(sweep_families(reports, arguments.minimum_speedup), indent=1))
+        print(json.dumps(sweep_families(reports, arguments.minimum_speedup, arguments.minimum_runs), indent=1))
         return 0
     if arguments.sweep is not None:
         start, stop, step = (int(v) for v in arguments.rows.split(":"))

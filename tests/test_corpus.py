@@ -170,6 +170,11 @@ def test_sweep_families_group_by_scheme_mode_and_pair() -> None:
             for f in combined] == [(True, 480, 480, 2, 1.1), (True, 1248, 1248, 2, 1.06)]
     document = C.dispatch_document(reports + second, 1.0, "test")
     assert document["families"] == combined and document["minimum_speedup"] == 1.0
+    # with two runs required, a row measured once never wins: 1248 rows of the second
+    # run missing leaves only 480 rows as a prepacked family
+    partial = C.sweep_families(reports + second[:2], 1.0, minimum_runs=2)
+    assert [(f["prepacked"], f["minimum_rows"], f["maximum_rows"], f["runs"]) for f in partial] == [(True, 480, 480, 2)]
+    assert C.dispatch_document(reports + second[:2], 1.0, "test", minimum_runs=2)["families"] == partial
     case = C.sweep_case(12288, 4608, True, 480)
     assert case.shape == (480, 12288, 4608) and case.bias and case.compute_dtype == "float16"
 
